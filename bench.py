@@ -1,0 +1,251 @@
+#!/usr/bin/env python3
+"""Benchmark of the TileGen HIP CSR hot path on one MI355X; prints ONE JSON line.
+
+A step is one launch of the case's tuned HIP variant over one copy of the
+case's inputs, already resident in HBM.  Launches rotate over enough input
+copies (>= 640 MB in total, more than the 256 MB Infinity Cache) that every
+step reads its matrix from HBM, not from a cache a previous step warmed.
+
+value        whole-job throughput: compulsory bytes of K steps / host wall time
+             of the K steps, bracketed by device synchronizations (launch gaps
+             included)
+roofline     per-kernel duration from start/stop events attached to each
+             dispatch (hipExtModuleLaunchKernel), averaged over the timed
+             launches; achieved = compulsory bytes per launch / that duration,
+             against MI355X's 8 TB/s HBM peak; traffic = HBM bytes per launch
+             measured with rocprofv3 FETCH_SIZE/WRITE_SIZE (profiles/), when a
+             summary for this kernel and case is committed
+cpu_baseline the reference's own sequential cpp/src/ref.cpp (oracle/_ref, kind
+             "reference"; else this repository's C restatement, kind "port"),
+             one host core, on the full case matrix for a bounded number of calls
+
+Cases are BASELINE.json's configs (tilegen_amd.matrices.baseline_ids()); the
+default c1 is the config the headline metric is quoted on.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "SpMV achieved HBM GB/s (% of peak) + GFLOP/s, fp64 CSR; SpMM/SDDMM GFLOP/s"
+PEAK_HBM_GBS = 8000.0
+ROTATE_BYTES = 640 << 20
+
+
+def _log(msg: str) -> None:
+    print("[bench] " + msg, file=sys.stderr, flush=True)
+
+
+def _parse_config(text: str):
+    from tilegen_amd.codegen import Config
+    vals = {}
+    for part in text.replace(",", "/").split("/"):
+        part = part.strip()
+        for key, name in (("TPR", "threads_per_row"), ("T", "tile_size"), ("U", "unroll"),
+                          ("V", "vector_width"), ("B", "block_size")):
+            if part.startswith(key) and part[len(key):].isdigit():
+                vals[name] = int(part[len(key):])
+                break
+        else:
+            raise SystemExit("bad --config component %r (want T128/TPR8/U2/V1/B256)" % part)
+    return Config(**vals)
+
+
+def _traffic(kernel: str, case_id: str):
+    """HBM bytes per launch from a committed rocprofv3 PMC summary, or None."""
+    path = os.path.join(ROOT, "profiles", "%s_%s_pmc.json" % (kernel, case_id))
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        d = json.load(fh)
+    return d.get("hbm_bytes_per_launch")
+
+
+def _cpu_baseline(kernel, A, ops, budget_s: float):
+    import oracle
+    kind = "reference" if oracle.reference_available() else "port"
+    M, N = A.shape
+    if kind == "reference":
+        rm = oracle.RefMatrix(A)
+        K = ops[next(iter(ops))].shape[1] if kernel != "spmv" else 0
+        rm.set_operands(K=K, x=ops.get("x"), B=ops.get("B"), U=ops.get("U"), V=ops.get("V"))
+        _, t1 = rm.run(kernel, 1)
+        iters = int(max(1, min(2000, budget_s / max(t1, 1e-6))))
+        _, sec = rm.run(kernel, iters)
+        rm.close()
+    else:
+        t0 = time.perf_counter()
+        oracle.compute(kernel, A, ops)
+        t1 = time.perf_counter() - t0
+        iters = int(max(1, min(2000, budget_s / max(t1, 1e-6))))
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            oracle.compute(kernel, A, ops)
+        sec = (time.perf_counter() - t0) / iters
+    return kind, sec, iters
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--case", default="c1")
+    ap.add_argument("--config", default=None, help="schedule override, e.g. T128/TPR8/U2/V1/B256")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="bound on the CPU baseline's timed calls")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--warm", action="store_true",
+                    help="no input rotation (cache-warm figure, reported as such)")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1:
+        print("bench.py runs on exactly one GPU: this build has no multi-GPU path "
+              "(--gpus %d requested). Run with --gpus 1." % args.gpus, file=sys.stderr)
+        return 2
+
+    from tilegen_amd import runtime as rt
+    from tilegen_amd.matrices import (baseline_case, baseline_operands, compulsory_bytes,
+                                      flops, make_baseline)
+    from tilegen_amd.schedules import TUNED
+    from tilegen_amd.variant import Variant
+
+    case = baseline_case(args.case)
+    cfg = _parse_config(args.config) if args.config else TUNED[args.case]
+    t_gen = time.time()
+    A = make_baseline(args.case)
+    M, N = A.shape
+    nnz = int(A.nnz)
+    K = case.K
+    ops = baseline_operands(case.kernel, M, N, K)
+    _log("case %s (%s) M=%d N=%d nnz=%d K=%d generated in %.1fs" % (
+        args.case, case.kernel, M, N, nnz, K, time.time() - t_gen))
+
+    if rt.device_count() < 1:
+        raise SystemExit("no HIP device visible")
+    dev = rt.device_info(0)
+    v = Variant(case.kernel, cfg)
+    fn = v.function()
+    grid, block, lds = v.geometry(M, N, K, nnz)
+    attrs = v.attrs()
+    _log("device %s (%s, %d CUs); variant %s grid=%d block=%d lds=%d %s" % (
+        dev["name"], dev["arch"], dev["cu_count"], cfg.short(), grid, block, lds, attrs))
+
+    nbytes = compulsory_bytes(case.kernel, M, N, nnz, K)
+    nflop = flops(case.kernel, nnz, K)
+    copies = 1 if args.warm else int(min(64, max(2, -(-ROTATE_BYTES // nbytes))))
+
+    host = {"indptr": A.indptr.astype(np.int64), "indices": A.indices.astype(np.int64),
+            "data": A.data.astype(np.float64)}
+    host.update({k: np.ascontiguousarray(val, dtype=np.float64) for k, val in ops.items()})
+    out_name = {"spmv": "y", "spmm": "C", "sddmm": "C"}[case.kernel]
+    out_shape = {"spmv": (M,), "spmm": (M, K), "sddmm": (nnz,)}[case.kernel]
+    sets, keep = [], []
+    for c in range(copies):
+        bufs = {k: rt.DeviceBuffer(a) for k, a in host.items()}
+        bufs[out_name] = rt.DeviceBuffer(np.zeros(out_shape))
+        keep.append(bufs)
+        sets.append(v.abi_values(A, bufs, {}, M, N, K, nnz))
+    _log("%d input copies resident (%.0f MB)" % (copies, copies * nbytes / 1e6))
+
+    # one checked launch through the C ABI before timing
+    v.device_call(sets[0])
+    got = keep[0][out_name].to_host()
+    import scipy.sparse  # noqa: F401  (float64 check of this run, not the oracle)
+    if case.kernel == "spmv":
+        ref = A @ ops["x"]
+    elif case.kernel == "spmm":
+        ref = A @ ops["B"]
+    else:
+        coo = A.tocoo()
+        ref = np.einsum("ik,ik->i", ops["U"][coo.row], ops["V"][coo.col]) * coo.data
+    err = float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-300))
+    _log("check vs float64 SciPy: normwise rel err %.3e" % err)
+    if not err <= 1e-10:
+        raise SystemExit("result check failed: rel err %.3e" % err)
+
+    arg_sets = rt.ArgSets(sets)
+    rt.run_launches(fn, grid, block, lds, arg_sets, args.warmup)
+    rt.synchronize()
+    t0 = time.perf_counter()
+    rt.run_launches(fn, grid, block, lds, arg_sets, args.steps)
+    rt.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall / args.steps * 1e3
+    value = nbytes * args.steps / wall / 1e9
+
+    kms, ev_wall_ms = rt.time_launches(fn, grid, block, lds, sets, args.warmup, args.steps)
+    k_avg_s = float(kms.mean()) * 1e-3
+    k_med_s = float(np.median(kms)) * 1e-3
+    achieved = nbytes / k_avg_s / 1e9
+    _log("timed %d steps: %.3f ms/step (host clock), kernel avg %.2f us median %.2f us, "
+         "events wall %.3f ms/step" % (args.steps, ms_per_step, k_avg_s * 1e6, k_med_s * 1e6,
+                                        ev_wall_ms / args.steps))
+
+    cpu = None
+    if not args.no_cpu:
+        kind, sec, iters = _cpu_baseline(case.kernel, A, ops, args.cpu_seconds)
+        cpu = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
+               "sample": "%d sequential calls of the full %s matrix (%d rows, %d nnz), "
+                         "%.3f ms per call" % (iters, args.case, M, nnz, sec * 1e3),
+               "gflops": round(nflop / sec / 1e9, 3), "ms_per_call": round(sec * 1e3, 4)}
+        _log("cpu baseline (%s): %.3f ms per call" % (kind, sec * 1e3))
+
+    for bufs in keep:
+        for b in bufs.values():
+            b.free()
+
+    unit = "GB/s"
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic (seeded BASELINE config generator, U(-1,1) values)",
+        "config": {
+            "workload": "%s: %s" % (args.case, case.description),
+            "case": args.case, "kernel": case.kernel, "rows": M, "cols": N, "nnz": nnz,
+            "K": K, "schedule": cfg.short(), "grid": grid, "block": block,
+            "input_copies": copies, "cache": "warm" if args.warm else "cold (rotated)",
+            "compulsory_bytes": nbytes,
+        },
+        "gflops": round(nflop * args.steps / wall / 1e9, 3),
+        "pct_of_peak_hbm": round(100.0 * value / PEAK_HBM_GBS, 2),
+        "kernel_us_avg": round(k_avg_s * 1e6, 3),
+        "kernel_us_median": round(k_med_s * 1e6, 3),
+        "kernel_gbs_median": round(nbytes / k_med_s / 1e9, 2),
+        "kernel_gflops_avg": round(nflop / k_avg_s / 1e9, 3),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": _traffic(case.kernel, args.case),
+        },
+        "cpu_baseline": cpu,
+        "check_rel_err": err,
+        "device": "%s %s" % (dev["name"], dev["arch"]),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

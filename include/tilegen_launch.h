@@ -1,0 +1,60 @@
+/*
+ * tilegen_launch.h -- the per-kernel launch ABI every generated HIP variant
+ * library exports (one shared object per (kernel, schedule), produced by
+ * tilegen_amd.verify.compile_generated).
+ *
+ * The three launch_* entry points are the reference's plugin interface for the
+ * CSR hot path, with identical argument order and types: each reference
+ * variant is one `extern "C" void launch_<name>(...)` (reference
+ * tilegen/codegen.py:226-280 `_abi`, :814-818; ctypes argtypes at
+ * tilegen/verify.py:166-173 `_SIGNATURES`; dlsym binding at
+ * cpp/src/harness.cpp:130-141).
+ *
+ * Contract (same as the reference's device path, verify.py:155-163):
+ *   - every pointer is a device pointer the caller allocated;
+ *   - indptr has M+1 entries, indices/data have nnz; indptr/indices are
+ *     never written;
+ *   - the call is synchronous (returns after the kernel finished);
+ *   - it returns void: a failure is recorded and reported by tg_last_status()
+ *     / tg_last_error() of libtgrt (the reference surfaces device errors at
+ *     its next synchronizing call);
+ *   - spmm: every element of C is written (C = A*B). The reference adds into
+ *     C (C += A*B) and all its callers pass C zeroed; both give A*B there.
+ *
+ * The tgv_* functions let a harness time or stream the same kernel without
+ * the synchronizing wrapper.
+ */
+#ifndef TILEGEN_LAUNCH_H
+#define TILEGEN_LAUNCH_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* y[i] = sum_p data[p] * x[indices[p]], p in [indptr[i], indptr[i+1]) */
+void launch_spmv(const int64_t* indptr, const int64_t* indices, const double* data,
+                 const double* x, double* y, int64_t M, int64_t N, int64_t nnz);
+
+/* C[i,:] = sum_p data[p] * B[indices[p], :]; B is N x K, C is M x K, row-major */
+void launch_spmm(const int64_t* indptr, const int64_t* indices, const double* data,
+                 const double* B, double* C, int64_t M, int64_t N, int64_t K,
+                 int64_t nnz);
+
+/* C[p] = data[p] * sum_k U[i,k] * V[indices[p],k]; U is M x K, V is N x K */
+void launch_sddmm(const int64_t* indptr, const int64_t* indices, const double* data,
+                  const double* U, const double* V, double* C, int64_t M, int64_t N,
+                  int64_t K, int64_t nnz);
+
+/* Harness side of a variant library (no counterpart in the reference). */
+void* tgv_function(void);                  /* the variant's kernel, current device */
+const char* tgv_kernel_name(void);         /* "spmv", "spmm", ... */
+int tgv_geometry(int64_t M, int64_t N, int64_t K, int64_t nnz, int64_t* grid,
+                 int32_t* block, int32_t* lds_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TILEGEN_LAUNCH_H */

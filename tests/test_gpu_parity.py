@@ -1,0 +1,141 @@
+"""GPU parity: every HIP variant against the C oracle and float64 SciPy.
+
+All launches go through the variant library's C ABI ``launch_<name>`` with
+device pointers.  The bar: normwise relative error <= 1e-10 (inf- and 2-norm)
+against both checkers, the reference tolerance from verify(), and indptr /
+indices byte-identical after the launch.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import scipy.sparse as sp
+
+import oracle
+from tests.util import csr, mixed_257, ragged, rel_2, rel_inf
+from tilegen_amd.codegen import Config
+from tilegen_amd.schedules import TEST_KERNELS, TEST_SCHEDULES, schedule_id
+from tilegen_amd.variant import Variant
+from tilegen_amd.verify import _inputs_for, _reference, verify
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-10  # normwise relative error bar
+
+
+def _operands(kernel, A, K, seed=7):
+    x, w, B, U, V, alpha, beta = _inputs_for(kernel, A, K, seed)
+    return {"x": x, "w": w, "B": B, "U": U, "V": V, "alpha": alpha, "beta": beta}
+
+
+def _oracle(kernel, A, ops):
+    if kernel == "axpy":
+        return oracle.axpy(ops["x"], ops["w"], ops["alpha"], ops["beta"])
+    return oracle.compute(kernel, A, ops)
+
+
+def _check(kernel, cfg, A, K, label=""):
+    ops = _operands(kernel, A, K)
+    v = Variant(kernel, cfg)
+    if kernel == "axpy":
+        out = v.run(None, x=ops["x"], w=ops["w"], alpha=ops["alpha"], beta=ops["beta"])
+    else:
+        out = v.run(A, **ops)
+    want = _oracle(kernel, A, ops)
+    sci = _reference(kernel, A, (ops["x"], ops["w"], ops["B"], ops["U"], ops["V"],
+                                 ops["alpha"], ops["beta"]))
+    for name, ref in (("oracle", want), ("scipy", sci)):
+        ri, r2 = rel_inf(out, ref), rel_2(out, ref)
+        assert ri <= TOL and r2 <= TOL, "%s %s %s vs %s: rel_inf=%g rel_2=%g" % (
+            kernel, cfg.short(), label, name, ri, r2)
+    return out
+
+
+@pytest.mark.parametrize("kernel", TEST_KERNELS)
+@pytest.mark.parametrize("cfg", TEST_SCHEDULES, ids=[schedule_id(c) for c in TEST_SCHEDULES])
+def test_verify_matches_float64_reference(kernel, cfg, hip_ready, tmp_path):
+    r = verify(kernel, cfg, mixed_257(), backend="hip", workdir=str(tmp_path), K=8)
+    assert r.executed, r.message
+    assert r.ok, "%s %s: %s" % (kernel, cfg.short(), r.message)
+    assert r.max_abs_err <= r.tolerance
+    assert r.rel_err_inf <= TOL and r.rel_err_2 <= TOL
+    if kernel != "axpy":
+        assert r.structure_intact is True
+
+
+@pytest.mark.parametrize("kernel", TEST_KERNELS)
+@pytest.mark.parametrize("cfg", TEST_SCHEDULES, ids=[schedule_id(c) for c in TEST_SCHEDULES])
+def test_matches_oracle_k64(kernel, cfg, hip_ready):
+    _check(kernel, cfg, mixed_257(), K=64)
+
+
+@pytest.mark.parametrize("kernel", ["spmm", "sddmm"])
+@pytest.mark.parametrize("K", [1, 7, 63, 130])
+def test_odd_and_wide_K(kernel, K, hip_ready):
+    """K not a multiple of the vector width (scalar fallback) and K wider than
+    one pass of the lanes."""
+    for cfg in (Config(tile_size=8, threads_per_row=32, unroll=4, vector_width=2,
+                       block_size=256),
+                Config(tile_size=4, threads_per_row=4, unroll=2, vector_width=2,
+                       block_size=256)):
+        _check(kernel, cfg, mixed_257(), K=K, label="K=%d" % K)
+
+
+@pytest.mark.parametrize("kernel", TEST_KERNELS)
+def test_injected_bug_is_caught(kernel, hip_ready, tmp_path):
+    cfg = Config(tile_size=32, threads_per_row=4, unroll=2, vector_width=1, block_size=256,
+                 inject_bug=True)
+    r = verify(kernel, cfg, mixed_257(), backend="hip", workdir=str(tmp_path), K=8)
+    assert r.executed and "compile error" not in r.message, r.message
+    assert not r.ok, "%s: injected bug not detected" % kernel
+    assert r.max_abs_err > r.tolerance
+
+
+SPMV_CFGS = [
+    Config(tile_size=128, threads_per_row=8, unroll=2, block_size=256),
+    Config(tile_size=64, threads_per_row=64, unroll=4, block_size=256),
+    Config(tile_size=256, threads_per_row=1, unroll=3, block_size=256),
+    Config(tile_size=32, threads_per_row=16, unroll=1, block_size=64),
+]
+
+
+@pytest.mark.parametrize("cfg", SPMV_CFGS, ids=[schedule_id(c) for c in SPMV_CFGS])
+def test_edge_cases_spmv(cfg, hip_ready):
+    cases = {
+        "no_nonzeros": csr(100, 50, np.zeros(101, dtype=np.int64), [], []),
+        "single": csr(1, 1, [0, 1], [0], [2.5]),
+        "one_long_row": ragged(3, 300, 40000, 0, long_rows=[(150, 25000)]),
+        "long_and_short": ragged(4, 2000, 6000, 9, empty_every=5,
+                                 long_rows=[(0, 5000), (1999, 3001), (777, 1)]),
+        "last_row_to_nnz_end": csr(3, 5, [0, 1, 2, 7], [0, 1, 0, 1, 2, 3, 4],
+                                   [1, 2, 3, 4, 5, 6, 7]),
+    }
+    for label, A in cases.items():
+        _check("spmv", cfg, A, K=1, label=label)
+
+
+def test_zero_rows(hip_ready):
+    A = sp.csr_matrix((np.zeros(0), np.zeros(0, dtype=np.int64), np.zeros(1, dtype=np.int64)),
+                      shape=(0, 4))
+    v = Variant("spmv", Config(tile_size=128, threads_per_row=8, unroll=2, block_size=256))
+    out = v.run(A, x=np.ones(4))
+    assert out.shape == (0,)
+
+
+def test_spmm_overwrites_output(hip_ready):
+    """C is output-only: prior contents (even NaN) never leak into the result."""
+    A = mixed_257()
+    ops = _operands("spmm", A, 64)
+    v = Variant("spmm", Config(tile_size=8, threads_per_row=32, unroll=4, vector_width=2,
+                               block_size=256))
+    out = v.run(A, out=np.full((A.shape[0], 64), np.nan), B=ops["B"])
+    assert np.isfinite(out).all()
+    assert rel_inf(out, oracle.spmm(A, ops["B"])) <= TOL
+
+
+def test_sddmm_empty_rows_and_long_rows(hip_ready):
+    A = ragged(9, 500, 700, 40, empty_every=3, long_rows=[(10, 600)])
+    for cfg in (Config(tile_size=4, threads_per_row=4, unroll=2, vector_width=2, block_size=256),
+                Config(tile_size=1, threads_per_row=64, unroll=1, vector_width=1, block_size=64)):
+        _check("sddmm", cfg, A, K=64)

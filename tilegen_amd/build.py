@@ -1,0 +1,97 @@
+"""Build everything native, in-tree: ``python -m tilegen_amd.build``.
+
+1. ``tilegen_amd/_lib/libtgrt.so`` (the runtime, include/tgrt.h) with the host
+   C++ compiler against the ROCm HIP runtime and hipRTC;
+2. the test oracle (``oracle/Makefile``: the C restatement, and the
+   reference's own ref.cpp where its sources are present);
+3. the hipRTC code objects and C launchers of every named schedule
+   (``schedules.TUNED`` and ``TEST_SCHEDULES``) into the kernel cache, so GPU
+   runs load prebuilt variants instead of compiling.  hipRTC needs no GPU.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+import time
+from typing import List, Optional
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(PKG)
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+
+
+def _run(cmd: List[str], cwd: Optional[str] = None) -> None:
+    res = subprocess.run(cmd, cwd=cwd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("command failed (%d): %s\n%s%s" % (res.returncode, " ".join(cmd),
+                                                              res.stdout, res.stderr))
+
+
+def build_runtime() -> str:
+    out_dir = os.path.join(PKG, "_lib")
+    os.makedirs(out_dir, exist_ok=True)
+    out = os.path.join(out_dir, "libtgrt.so")
+    tmp = out + ".tmp%d" % os.getpid()
+    cxx = os.environ.get("CXX") or shutil.which("g++") or "c++"
+    _run([cxx, "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-D__HIP_PLATFORM_AMD__",
+          "-I", os.path.join(REPO, "include"), "-I", os.path.join(ROCM, "include"),
+          os.path.join(PKG, "csrc", "tgrt.cpp"), "-o", tmp, "-Wl,-soname,libtgrt.so",
+          "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-lhiprtc",
+          "-Wl,-rpath," + os.path.join(ROCM, "lib")])
+    os.replace(tmp, out)
+    return out
+
+
+def build_oracle() -> None:
+    _run(["make", "-s", "-C", os.path.join(REPO, "oracle")])
+
+
+def warm_cache(verbose: bool = False) -> int:
+    """Compile every named schedule for every kernel it applies to."""
+    from . import runtime
+    runtime._LIB = None  # pick up a freshly built library
+    from .codegen import Config, generate
+    from .dsl import standard_kernels
+    from .matrices import baseline_case
+    from .schedules import TEST_KERNELS, TEST_SCHEDULES, TUNED
+    from .verify import compile_generated
+
+    kernels = standard_kernels()
+    todo = []
+    for case_id, cfg in TUNED.items():
+        todo.append((baseline_case(case_id).kernel, cfg))
+    for name in TEST_KERNELS:
+        for cfg in TEST_SCHEDULES:
+            todo.append((name, cfg))
+        todo.append((name, Config(tile_size=32, threads_per_row=4, unroll=2, vector_width=1,
+                                  block_size=256, inject_bug=True)))
+    workdir = os.path.join(REPO, "build", "generated")
+    n = 0
+    for name, cfg in todo:
+        gen = generate(kernels[name], cfg, "hip", outdir=workdir)
+        compile_generated(gen, "hip", workdir)
+        n += 1
+        if verbose:
+            print("[build] %s %s" % (name, cfg.short()))
+    return n
+
+
+def build_all(verbose: bool = True) -> None:
+    t0 = time.time()
+    path = build_runtime()
+    if verbose:
+        print("[build] runtime %s (%.1fs)" % (path, time.time() - t0))
+    build_oracle()
+    if verbose:
+        print("[build] oracle (%.1fs)" % (time.time() - t0))
+    n = warm_cache()
+    if verbose:
+        print("[build] %d HIP variants cached (%.1fs)" % (n, time.time() - t0))
+
+
+if __name__ == "__main__":
+    build_all(verbose=True)
+    sys.exit(0)

@@ -1,0 +1,1178 @@
+"""Code generation: the HIP (gfx950) emitter and the OpenMP CPU emitter.
+
+``generate(kernel, config, backend)`` runs the pass pipeline and renders one
+translation unit per variant; every variant exposes the reference ABI
+``extern "C" void launch_<name>(...)`` (reference ``codegen.py:226-280``).
+
+backend "hip"
+    ``GeneratedKernel.source`` is device code only (one ``extern "C"
+    __global__`` kernel plus small wave64 helpers), compiled at run time by
+    hipRTC for gfx950.  ``GeneratedKernel.host_source`` is a C launcher that
+    embeds the compiled code object and exports ``launch_<name>`` with the
+    reference argument list, plus ``tgv_geometry``/``tgv_function`` for timing
+    harnesses.  The device code is written for CDNA4, not translated:
+
+    scalar_reduce (spmv, fused_spmv_axpy)
+        ThreadsPerRow(k) lanes per row with a segmented DPP butterfly over k
+        lanes of a 64-lane wave; Unroll(u) = each lane owns u consecutive
+        nonzeros per step, loaded as 128-bit pairs from a 16-byte aligned base
+        (row starts are rounded down, the extra lanes masked); Tile(T) = a
+        workgroup owns T rows whose row pointers are staged once in LDS and
+        whose first step is issued for every row before any gather, so each
+        wave keeps several rows of loads in flight.
+    row_dense_out (spmm)
+        ThreadsPerRow(k) lanes per output row spread over the K columns,
+        Vectorize(2) = 128-bit loads of B rows and stores of C, Unroll(u) =
+        u nonzeros' B rows in flight.  With k = 64 the row is wave-uniform and
+        (column, value) pairs arrive through the scalar unit.  C is written
+        exactly once per element (no read-modify-write).
+    sparse_out (sddmm)
+        one wave per row; ThreadsPerRow(k) lanes split the K-long dot product
+        of one nonzero (64/k nonzeros per wave at once), Vectorize(2) =
+        128-bit loads of U and V rows, Unroll(u) = u K-chunks in flight.
+    elementwise (axpy)
+        one lane per element.
+
+backend "cpu"
+    OpenMP C++ restating reference ``_cpu_emit`` (``codegen.py:354-558``): the
+    CPU baseline.  One deliberate change: the ``#pragma omp simd`` of spmm
+    with vector_width > 1 is placed directly on the loop it vectorizes (the
+    reference puts it before a declaration, which fails under -fopenmp and
+    makes its compile retry silently without OpenMP).
+
+``inject_bug=True`` makes every emitter stop one row short (the last row is
+never written), so the differential tester can show it catches wrong kernels.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import os
+from dataclasses import dataclass, field
+from typing import Any, Callable, Dict, List, Optional, Sequence, Tuple
+
+from . import passes as _passes
+from .ir import (
+    Access, Add, Const, Expr, Fuse, Index, Kernel, Mul, Parallelize, Reduce, Split,
+    ThreadsPerRow, Tile, Unroll, Vectorize,
+)
+
+__all__ = [
+    "Config", "GeneratedKernel", "Lowering", "Plan", "LaunchGeometry", "generate",
+    "emit_hip", "emit_hip_host", "emit_cpu", "launch_geometry", "abi_of",
+    "HIP_ARCH", "WAVE",
+]
+
+HIP_ARCH = os.environ.get("TILEGEN_HIP_ARCH", "gfx950")
+WAVE = 64
+
+_CTYPE = {"f64": "double", "f32": "float", "double": "double", "float": "float"}
+
+
+def ctype(dtype: str) -> str:
+    return _CTYPE.get(dtype, "double")
+
+
+# --------------------------------------------------------------------------- #
+# Config / Lowering
+# --------------------------------------------------------------------------- #
+@dataclass
+class Config:
+    """Flat schedule request; the passes lower it into the schedule IR.
+
+    tile_size T (rows per workgroup), threads_per_row TPR, unroll U,
+    vector_width V, block_size B (lanes per workgroup).
+    """
+
+    tile_size: int = 32
+    threads_per_row: int = 1
+    unroll: int = 1
+    vector_width: int = 1
+    block_size: int = 256
+    dtype: str = "f64"
+    inject_bug: bool = False
+
+    def to_dict(self) -> Dict[str, Any]:
+        return {"tile_size": self.tile_size, "threads_per_row": self.threads_per_row,
+                "unroll": self.unroll, "vector_width": self.vector_width,
+                "block_size": self.block_size, "dtype": self.dtype,
+                "inject_bug": self.inject_bug}
+
+    def hash(self) -> str:
+        """sha1 of ``T|TPR|U|V|B|dtype|bug``, 10 hex digits (the reference's
+        closed form, ``codegen.py:82-87``, so cache names line up)."""
+        key = "%d|%d|%d|%d|%d|%s|%d" % (self.tile_size, self.threads_per_row, self.unroll,
+                                        self.vector_width, self.block_size, self.dtype,
+                                        int(self.inject_bug))
+        return hashlib.sha1(key.encode()).hexdigest()[:10]
+
+    def short(self) -> str:
+        return "T%d/TPR%d/U%d/V%d/B%d" % (self.tile_size, self.threads_per_row,
+                                          self.unroll, self.vector_width, self.block_size)
+
+
+@dataclass
+class Lowering:
+    """What the emitters read: the schedule transforms folded into numbers.
+
+    ``tiled`` records whether a Tile transform is present (untiled HIP kernels
+    read row pointers straight from global memory; tiled ones stage them).
+    """
+
+    tile: int = 1
+    threads_per_row: int = 1
+    unroll: int = 1
+    vector_width: int = 1
+    block_size: int = 256
+    parallel: bool = False
+    tiled: bool = False
+
+    def to_dict(self) -> Dict[str, Any]:
+        return {"tile": self.tile, "threads_per_row": self.threads_per_row,
+                "unroll": self.unroll, "vector_width": self.vector_width,
+                "block_size": self.block_size, "parallel": self.parallel}
+
+
+def _lowering(kernel: Kernel) -> Lowering:
+    low = Lowering()
+    for t in kernel.schedule:
+        if isinstance(t, Tile):
+            low.tile, low.tiled = t.size, True
+        elif isinstance(t, ThreadsPerRow):
+            low.threads_per_row = t.k
+        elif isinstance(t, Unroll):
+            low.unroll = t.factor
+        elif isinstance(t, Vectorize):
+            low.vector_width = t.width
+        elif isinstance(t, Parallelize):
+            low.parallel = True
+            if t.block_size:
+                low.block_size = t.block_size
+    return low
+
+
+@dataclass
+class LaunchGeometry:
+    """Grid rule of a HIP variant: ``grid = ceil(rows / rows_per_block)``."""
+
+    rows_per_block: int
+    block: int
+    lds_bytes: int
+    rows_symbol: str = "M"
+
+    def grid(self, rows: int) -> int:
+        return (int(rows) + self.rows_per_block - 1) // self.rows_per_block if rows > 0 else 0
+
+    def to_dict(self) -> Dict[str, Any]:
+        return {"rows_per_block": self.rows_per_block, "block": self.block,
+                "lds_bytes": self.lds_bytes, "rows_symbol": self.rows_symbol}
+
+
+@dataclass
+class GeneratedKernel:
+    source: str
+    filename: str
+    abi_signature: str
+    pass_log: List[Dict[str, Any]] = field(default_factory=list)
+    backend: str = "cpu"
+    kernel_name: str = ""
+    config: Optional[Config] = None
+    #: HIP only: the C launcher text (a ``{CODE_OBJECT}`` placeholder stands
+    #: where the compiled bytes are embedded), the device symbol and geometry.
+    host_source: str = ""
+    device_symbol: str = ""
+    geometry: Optional[LaunchGeometry] = None
+    abi_args: List[Tuple[str, str]] = field(default_factory=list)
+
+    def write(self, outdir: str = "build/generated") -> str:
+        os.makedirs(outdir, exist_ok=True)
+        path = os.path.join(outdir, self.filename)
+        with open(path, "w") as fh:
+            fh.write(self.source)
+        return path
+
+
+# --------------------------------------------------------------------------- #
+# plan: what shape of loop nest the statement needs (reference codegen.py:158-220)
+# --------------------------------------------------------------------------- #
+@dataclass
+class Plan:
+    kind: str  # scalar_reduce | row_dense_out | sparse_out | elementwise
+    out: Access
+    out_tensor: Any
+    A: Optional[Any] = None
+    row_idx: Optional[Index] = None
+    col_idx: Optional[Index] = None
+    reduce: Optional[Reduce] = None
+    reduce_is_compressed: bool = False
+    inner_out: List[Index] = field(default_factory=list)
+    value_expr: Optional[Expr] = None
+    final_expr: Optional[Expr] = None
+    row_extent: str = "M"
+
+
+def _plan(kernel: Kernel) -> Plan:
+    stmt = kernel.stmts[0]
+    out = stmt.lhs
+    A = kernel.sparse_tensor()
+    red = kernel.reduce_node()
+    if A is None:
+        return Plan(kind="elementwise", out=out, out_tensor=out.tensor,
+                    value_expr=stmt.rhs, final_expr=stmt.rhs,
+                    row_extent=str(out.tensor.shape[0]) if out.tensor.shape else "M")
+    a_acc = next(n for n in stmt.rhs.walk()
+                 if isinstance(n, Access) and n.tensor.name == A.name)
+    row_idx, col_idx = a_acc.indices[0], a_acc.indices[1]
+    over_nnz = red is not None and red.index.name == col_idx.name
+    inner = [ix for ix in out.indices if ix.name not in (row_idx.name, col_idx.name)]
+    if out.tensor.format.is_sparse():
+        kind = "sparse_out"
+    elif over_nnz and inner:
+        kind = "row_dense_out"
+    else:
+        kind = "scalar_reduce"
+    return Plan(kind=kind, out=out, out_tensor=out.tensor, A=A, row_idx=row_idx,
+                col_idx=col_idx, reduce=red, reduce_is_compressed=over_nnz,
+                inner_out=inner, value_expr=red.body if red is not None else stmt.rhs,
+                final_expr=stmt.rhs, row_extent=str(A.shape[0]) if A.shape else "M")
+
+
+# --------------------------------------------------------------------------- #
+# ABI (reference codegen.py:226-280): arrays in tensor discovery order (a sparse
+# input expands to indptr, indices, data), then scalars, then every symbolic
+# dimension in first-seen order, then nnz when a sparse tensor is present.
+# --------------------------------------------------------------------------- #
+def abi_of(kernel: Kernel) -> Tuple[str, List[Tuple[str, str]], Dict[str, Any]]:
+    """Return (signature, [(c_type, name)...], info)."""
+    out_name = kernel.stmts[0].lhs.tensor.name
+    dt = ctype(kernel.dtypes[0] if kernel.dtypes else "f64")
+    arrays: List[Tuple[str, Any]] = []
+    scalars, dims = [], []
+    n_sparse_in = 0
+    for t in kernel.tensors():
+        if t.order == 0:
+            scalars.append(t)
+            continue
+        if t.format.is_sparse():
+            if t.name == out_name:
+                arrays.append(("out_sparse", t))
+            else:
+                n_sparse_in += 1
+                arrays.append(("sparse", t))
+        else:
+            arrays.append(("dense", t))
+        for s in t.shape:
+            if str(s) not in dims:
+                dims.append(str(s))
+    if n_sparse_in > 1:
+        raise NotImplementedError("codegen supports at most one sparse input")
+    args: List[Tuple[str, str]] = []
+    for kind, t in arrays:
+        if kind == "sparse":
+            args += [("const int64_t*", "indptr"), ("const int64_t*", "indices"),
+                     ("const %s*" % dt, "data")]
+        elif kind == "out_sparse" or t.name == out_name:
+            args.append(("%s*" % dt, t.name))
+        else:
+            args.append(("const %s*" % dt, t.name))
+    args += [(dt, t.name) for t in scalars]
+    args += [("int64_t", d) for d in dims]
+    has_sparse = any(kind != "dense" for kind, _ in arrays)
+    if has_sparse:
+        args.append(("int64_t", "nnz"))
+    sig = "void launch_%s(%s)" % (kernel.name, ", ".join("%s %s" % a for a in args))
+    info = {"arrays": arrays, "scalars": [t.name for t in scalars], "dims": dims,
+            "dtype": kernel.dtypes[0] if kernel.dtypes else "f64",
+            "has_sparse": has_sparse, "decls": ["%s %s" % a for a in args]}
+    return sig, args, info
+
+
+def _abi(kernel: Kernel):
+    sig, _args, info = abi_of(kernel)
+    return sig, info, info["has_sparse"]
+
+
+# --------------------------------------------------------------------------- #
+# expressions -> C text
+# --------------------------------------------------------------------------- #
+def _fmt_const(v: float) -> str:
+    return "%.1f" % v if v == int(v) else repr(v)
+
+
+def _row_major_strides(shape) -> List[str]:
+    strides, acc = [], "1"
+    for s in reversed(shape):
+        strides.append(acc)
+        acc = str(s) if acc == "1" else "%s*%s" % (acc, s)
+    return list(reversed(strides))
+
+
+class _Env:
+    """Variable bindings for expression emission.
+
+    ``bind`` maps index names to C expressions, ``p`` is the current nonzero
+    position (None outside a compressed loop), ``acc`` the accumulator text
+    that stands for a Reduce node, ``data`` the text of the sparse value load.
+    """
+
+    def __init__(self, bind: Dict[str, str], p: Optional[str] = None,
+                 acc: Optional[str] = None, data: Optional[str] = None):
+        self.bind = dict(bind)
+        self.p = p
+        self.acc = acc
+        self.data = data
+
+    def with_(self, **kw) -> "_Env":
+        e = _Env(self.bind, self.p, self.acc, self.data)
+        for key, val in kw.items():
+            if key == "bind":
+                e.bind.update(val)
+            else:
+                setattr(e, key, val)
+        return e
+
+
+def _offset(t, indices: Sequence[Index], env: _Env) -> str:
+    terms = []
+    for ix, stride in zip(indices, _row_major_strides(t.shape)):
+        c = env.bind.get(ix.name, ix.name)
+        terms.append(c if stride == "1" else "(%s)*%s" % (c, stride))
+    return " + ".join(terms) if terms else "0"
+
+
+def _cexpr(e: Expr, env: _Env) -> str:
+    if isinstance(e, Access):
+        t = e.tensor
+        if t.order == 0:
+            return t.name
+        if t.format.is_sparse():
+            if env.p is None:
+                raise ValueError("sparse access %s outside a compressed loop" % t.name)
+            return env.data if env.data is not None else "data[%s]" % env.p
+        return "%s[%s]" % (t.name, _offset(t, e.indices, env))
+    if isinstance(e, Const):
+        return _fmt_const(e.value)
+    if isinstance(e, Mul):
+        return "(%s * %s)" % (_cexpr(e.left, env), _cexpr(e.right, env))
+    if isinstance(e, Add):
+        return "(%s + %s)" % (_cexpr(e.left, env), _cexpr(e.right, env))
+    if isinstance(e, Reduce):
+        if env.acc is None:
+            raise ValueError("Reduce encountered without an accumulator")
+        return env.acc
+    raise TypeError("cannot emit %r" % (e,))
+
+
+def _extent_for(plan: Plan, index_name: str) -> str:
+    """Extent of a dense index, read off any dense access that carries it."""
+    accesses: List[Access] = [plan.out]
+    for ex in (plan.value_expr, plan.final_expr):
+        if ex is not None:
+            accesses += [n for n in ex.walk() if isinstance(n, Access)]
+    for acc in accesses:
+        if acc.tensor.format.is_sparse():
+            continue
+        for pos, ix in enumerate(acc.indices):
+            if ix.name == index_name and pos < len(acc.tensor.shape):
+                return str(acc.tensor.shape[pos])
+    return "K"
+
+
+class _W:
+    """Indented line writer."""
+
+    def __init__(self):
+        self.lines: List[str] = []
+        self.depth = 0
+
+    def __call__(self, text: str = "") -> "_W":
+        self.lines.append(("  " * self.depth + text) if text else "")
+        return self
+
+    def open(self, text: str) -> "_W":
+        self(text + " {")
+        self.depth += 1
+        return self
+
+    def close(self, tail: str = "") -> "_W":
+        self.depth -= 1
+        self("}" + tail)
+        return self
+
+    def text(self) -> str:
+        return "\n".join(self.lines)
+
+
+# --------------------------------------------------------------------------- #
+# CPU (OpenMP) emitter -- the CPU baseline
+# --------------------------------------------------------------------------- #
+def _cpu_compressed_loop(w: _W, plan: Plan, env: _Env, unroll: int,
+                         body: Callable[[_W, _Env], None]) -> None:
+    """Loop over the row's nonzeros; unrolled by ``unroll`` with a scalar tail."""
+    row = env.bind[plan.row_idx.name]
+    w("int64_t p = indptr[%s];" % row)
+    w("int64_t pend = indptr[%s + 1];" % row)
+
+    def at(pos: str) -> _Env:
+        return env.with_(p=pos, bind={plan.col_idx.name: "indices[%s]" % pos})
+
+    if unroll > 1:
+        w("int64_t q = p;")
+        w.open("for (; q + %d <= pend; q += %d)" % (unroll, unroll))
+        for o in range(unroll):
+            w.open("")
+            body(w, at("q + %d" % o if o else "q"))
+            w.close()
+        w.close()
+        w.open("for (; q < pend; ++q)")
+        body(w, at("q"))
+        w.close()
+    else:
+        w.open("for (int64_t q = p; q < pend; ++q)")
+        body(w, at("q"))
+        w.close()
+
+
+def _cpu_dense_reduce(w: _W, extent: str, unroll: int, value: Callable[[str], str]) -> None:
+    if unroll > 1:
+        w("int64_t rq = 0;")
+        w.open("for (; rq + %d <= %s; rq += %d)" % (unroll, extent, unroll))
+        for o in range(unroll):
+            w("acc += %s;" % value("rq + %d" % o))
+        w.close()
+        w.open("for (; rq < %s; ++rq)" % extent)
+        w("acc += %s;" % value("rq"))
+        w.close()
+    else:
+        w.open("for (int64_t kr = 0; kr < %s; ++kr)" % extent)
+        w("acc += %s;" % value("kr"))
+        w.close()
+
+
+def _cpu_body(kernel: Kernel, config: Config, plan: Plan, low: Lowering) -> str:
+    dt = ctype(config.dtype)
+    tile = low.tile if low.tile > 1 else 1
+    unroll = low.unroll
+    bound = "(%s - 1)" % plan.row_extent if config.inject_bug else plan.row_extent
+    w = _W()
+
+    def rows(body: Callable[[_W, _Env], None]) -> None:
+        if low.parallel:
+            w("#pragma omp parallel for schedule(dynamic, 256)")
+        if tile > 1:
+            w.open("for (int64_t i_o = 0; i_o < %s; i_o += %d)" % (bound, tile))
+            w("int64_t i_hi = (i_o + %d < %s) ? i_o + %d : %s;" % (tile, bound, tile, bound))
+            w.open("for (int64_t i_i = i_o; i_i < i_hi; ++i_i)")
+            body(w, _Env({plan.row_idx.name: "i_i"}, acc="acc"))
+            w.close()
+            w.close()
+        else:
+            w.open("for (int64_t i = 0; i < %s; ++i)" % bound)
+            body(w, _Env({plan.row_idx.name: "i"}, acc="acc"))
+            w.close()
+
+    if plan.kind == "elementwise":
+        ix = plan.out.indices[0]
+        if low.parallel:
+            w("#pragma omp parallel for schedule(dynamic, 256)")
+        w.open("for (int64_t i = 0; i < %s; ++i)" % bound)
+        env = _Env({ix.name: "i"})
+        w("%s[%s] = %s;" % (plan.out_tensor.name, _offset(plan.out_tensor, plan.out.indices, env),
+                            _cexpr(plan.value_expr, env)))
+        w.close()
+
+    elif plan.kind == "scalar_reduce":
+        def row_body(w: _W, env: _Env) -> None:
+            w("%s acc = 0.0;" % dt)
+            if plan.reduce_is_compressed:
+                _cpu_compressed_loop(w, plan, env, unroll,
+                                     lambda w2, e2: w2("acc += %s;" % _cexpr(plan.value_expr, e2)))
+            else:
+                ext = _extent_for(plan, plan.reduce.index.name)
+
+                def per_nnz(w2: _W, e2: _Env) -> None:
+                    _cpu_dense_reduce(w2, ext, unroll, lambda kx: _cexpr(
+                        plan.value_expr, e2.with_(bind={plan.reduce.index.name: kx})))
+                _cpu_compressed_loop(w, plan, env, 1, per_nnz)
+            w("%s[%s] = %s;" % (plan.out_tensor.name,
+                                _offset(plan.out_tensor, plan.out.indices, env),
+                                _cexpr(plan.final_expr, env)))
+        rows(row_body)
+
+    elif plan.kind == "row_dense_out":
+        inner = plan.inner_out[0]
+        ext = _extent_for(plan, inner.name)
+
+        def write(w2: _W, e2: _Env, kx: str) -> None:
+            e3 = e2.with_(bind={inner.name: kx}, acc=None)
+            w2("%s[%s] += %s;" % (plan.out_tensor.name,
+                                  _offset(plan.out_tensor, plan.out.indices, e3),
+                                  _cexpr(plan.value_expr, e3)))
+
+        def per_nnz(w2: _W, e2: _Env) -> None:
+            simd = "#pragma omp simd" if low.vector_width > 1 else None
+            if unroll > 1:
+                w2("int64_t ku = 0;")
+                if simd:
+                    w2(simd)
+                w2.open("for (; ku + %d <= %s; ku += %d)" % (unroll, ext, unroll))
+                for o in range(unroll):
+                    write(w2, e2, "ku + %d" % o)
+                w2.close()
+                w2.open("for (; ku < %s; ++ku)" % ext)
+                write(w2, e2, "ku")
+                w2.close()
+            else:
+                if simd:
+                    w2(simd)
+                w2.open("for (int64_t k = 0; k < %s; ++k)" % ext)
+                write(w2, e2, "k")
+                w2.close()
+
+        rows(lambda w2, e2: _cpu_compressed_loop(w2, plan, e2, unroll, per_nnz))
+
+    elif plan.kind == "sparse_out":
+        ext = _extent_for(plan, plan.reduce.index.name)
+
+        def per_nnz(w2: _W, e2: _Env) -> None:
+            w2("%s acc = 0.0;" % dt)
+            _cpu_dense_reduce(w2, ext, unroll, lambda kx: _cexpr(
+                plan.value_expr, e2.with_(bind={plan.reduce.index.name: kx})))
+            w2("%s[%s] = %s;" % (plan.out_tensor.name, e2.p, _cexpr(plan.final_expr, e2)))
+
+        rows(lambda w2, e2: _cpu_compressed_loop(w2, plan, e2, 1, per_nnz))
+    else:  # pragma: no cover
+        raise NotImplementedError(plan.kind)
+    return w.text()
+
+
+# --------------------------------------------------------------------------- #
+# shared header
+# --------------------------------------------------------------------------- #
+def _transform_text(t) -> str:
+    if isinstance(t, Tile):
+        return "Tile(%s,%d)" % (t.index.name, t.size)
+    if isinstance(t, Split):
+        return "Split(%s,%d)" % (t.index.name, t.factor)
+    if isinstance(t, Parallelize):
+        return ("Parallelize(%s,%s,B%d)" % (t.index.name, t.unit, t.block_size)
+                if t.block_size else "Parallelize(%s,%s)" % (t.index.name, t.unit))
+    if isinstance(t, Unroll):
+        return "Unroll(%s,%d)" % (t.index.name, t.factor)
+    if isinstance(t, Fuse):
+        return "Fuse(%s,%s)" % (t.index_a.name, t.index_b.name)
+    if isinstance(t, ThreadsPerRow):
+        return "ThreadsPerRow(%d)" % t.k
+    if isinstance(t, Vectorize):
+        return "Vectorize(%d)" % t.width
+    return t.kind
+
+
+def _header(kernel: Kernel, config: Config, backend: str, low: Lowering,
+            extra: Sequence[str] = ()) -> str:
+    lines = [
+        "// TileGen generated kernel -- DO NOT EDIT BY HAND.",
+        "// kernel      : %s" % kernel.name,
+        "// backend     : %s" % backend,
+        "// config      : %s" % config.to_dict(),
+        "// lowering    : %s" % low.to_dict(),
+        "// schedule    : %s" % (", ".join(_transform_text(t) for t in kernel.schedule)
+                                 if len(kernel.schedule) else "(default)"),
+    ]
+    lines += ["// %s" % e for e in extra]
+    lines.append("// pass log    :")
+    lines += ["//   [%s] %s" % (e.get("pass"), e.get("action")) for e in kernel.pass_log] \
+        or ["//   (none)"]
+    return "\n".join(lines)
+
+
+def emit_cpu(kernel: Kernel, config: Config) -> str:
+    plan, low = _plan(kernel), _lowering(kernel)
+    sig, _args, _info = abi_of(kernel)
+    body = _cpu_body(kernel, config, plan, low)
+    return "\n".join([_header(kernel, config, "cpu", low), "#include <cstdint>",
+                      "#include <cstddef>", "", 'extern "C" %s {' % sig, body, "}", ""])
+
+
+# --------------------------------------------------------------------------- #
+# HIP emitter (gfx950, wave64)
+# --------------------------------------------------------------------------- #
+# Device helpers emitted into every HIP translation unit.  hipRTC provides the
+# HIP device builtins without any #include.
+_HIP_PRELUDE = r"""
+typedef long long tg_i64;
+typedef long long tg_i64x2 __attribute__((ext_vector_type(2)));
+typedef double tg_f64x2 __attribute__((ext_vector_type(2)));
+
+// Move a double between lanes with a DPP pattern (within a 16-lane row).
+template <int CTRL>
+__device__ __forceinline__ double tg_dpp(double v) {
+  const tg_i64 b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)b, CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, 0xF, 0xF, false);
+  return __longlong_as_double(((tg_i64)hi << 32) | (tg_i64)(unsigned)lo);
+}
+
+// Sum over each aligned group of W consecutive lanes (W divides 64); every lane
+// of a group ends with the group's sum.  Butterfly: quad_perm [1,0,3,2] and
+// [2,3,0,1], then row_half_mirror and row_mirror (lane i <-> 7-i, 15-i pair the
+// two halves once the halves are uniform), then swizzles across 16 and 32.
+template <int W>
+__device__ __forceinline__ double tg_segsum(double v) {
+  if (W >= 2) v += tg_dpp<0xB1>(v);
+  if (W >= 4) v += tg_dpp<0x4E>(v);
+  if (W >= 8) v += tg_dpp<0x141>(v);
+  if (W >= 16) v += tg_dpp<0x140>(v);
+  if (W >= 32) v += __shfl_xor(v, 16);
+  if (W >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+
+__device__ __forceinline__ tg_i64 tg_uniform(tg_i64 v) {
+  const int lo = __builtin_amdgcn_readfirstlane((int)v);
+  const int hi = __builtin_amdgcn_readfirstlane((int)(v >> 32));
+  return ((tg_i64)hi << 32) | (tg_i64)(unsigned)lo;
+}
+"""
+
+
+def _hip_decls(args: List[Tuple[str, str]]) -> str:
+    """Kernel parameter list: the ABI with restrict-qualified pointers."""
+    out = []
+    for ct, name in args:
+        ct = ct.replace("int64_t", "tg_i64")
+        if ct.endswith("*"):
+            out.append("%s __restrict__ %s" % (ct, name))
+        else:
+            out.append("const %s %s" % (ct, name))
+    return ", ".join(out)
+
+
+def launch_geometry(plan: Plan, low: Lowering) -> LaunchGeometry:
+    """Rows per workgroup and LDS bytes of the HIP variant for this schedule."""
+    B = min(low.block_size, 1024)
+    tpr = max(1, low.threads_per_row)
+    if plan.kind == "elementwise":
+        return LaunchGeometry(B, B, 0, plan.row_extent)
+    if plan.kind == "sparse_out":
+        rows = low.tile if low.tiled else max(1, B // WAVE)
+        return LaunchGeometry(rows, B, 0, plan.row_extent)
+    slots = max(1, B // tpr)
+    rows = low.tile if low.tiled else slots
+    lds = 8 * (rows + 1) if (plan.kind == "scalar_reduce" and low.tiled) else 0
+    return LaunchGeometry(rows, B, lds, plan.row_extent)
+
+
+def _check_hip_schedule(plan: Plan, low: Lowering) -> None:
+    B, tpr = low.block_size, low.threads_per_row
+    if B % WAVE or B <= 0 or B > 1024:
+        raise ValueError("HIP block_size must be a multiple of 64 in [64, 1024], got %d" % B)
+    if plan.kind != "elementwise":
+        if tpr < 1 or tpr > WAVE or WAVE % tpr:
+            raise ValueError("HIP threads_per_row must divide 64, got %d" % tpr)
+    if low.vector_width not in (1, 2, 4):
+        raise ValueError("vector_width %d not supported" % low.vector_width)
+    if low.unroll < 1 or low.unroll > 16:
+        raise ValueError("unroll must be in 1..16, got %d" % low.unroll)
+    if low.tiled and low.tile > 4096:
+        raise ValueError("tile_size %d exceeds 4096 rows per workgroup" % low.tile)
+
+
+def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeometry,
+                       out_name: str) -> None:
+    """y[row] = final(sum over the row's nonzeros of value_expr)."""
+    B, TPR = geo.block, max(1, low.threads_per_row)
+    U = max(1, low.unroll)
+    SLOTS = B // TPR
+    TR = geo.rows_per_block
+    R = (TR + SLOTS - 1) // SLOTS
+    ALIGN = 2 if U % 2 == 0 else 1
+    STEP = TPR * U
+    row = plan.row_idx.name
+    col = plan.col_idx.name
+
+    w("const tg_i64 row_end = %s;" % bound)
+    w("const tg_i64 row0 = (tg_i64)blockIdx.x * %d;" % TR)
+    w("const int lane = threadIdx.x %% %d;" % TPR)
+    w("const int slot = threadIdx.x / %d;" % TPR)
+    if low.tiled:
+        w("// row pointers of this tile, staged once in LDS")
+        w("__shared__ tg_i64 s_ptr[%d];" % (TR + 1))
+        w.open("for (int t = threadIdx.x; t <= %d; t += %d)" % (TR, B))
+        w("const tg_i64 r = row0 + t;")
+        w("s_ptr[t] = indptr[r < row_end ? r : row_end];")
+        w.close()
+        w("__syncthreads();")
+    w("tg_i64 rs[%d], re[%d];" % (R, R))
+    w("double acc[%d];" % R)
+    w("#pragma unroll")
+    w.open("for (int r = 0; r < %d; ++r)" % R)
+    w("const int lr = slot + r * %d;" % SLOTS)
+    w("const bool live = lr < %d && row0 + lr < row_end;" % TR)
+    if low.tiled:
+        w("const int li = lr < %d ? lr : 0;" % TR)
+        w("rs[r] = live ? s_ptr[li] : 0;")
+        w("re[r] = live ? s_ptr[li + 1] : 0;")
+    else:
+        w("const tg_i64 ri = live ? row0 + lr : 0;")
+        w("rs[r] = live ? indptr[ri] : 0;")
+        w("re[r] = live ? indptr[ri + 1] : 0;")
+    w("acc[r] = 0.0;")
+    w.close()
+
+    def step(q: str, r: str) -> None:
+        """Load U consecutive nonzeros at q (masked to the row), gather, FMA."""
+        w("tg_i64 ci[%d]; double cv[%d];" % (U, U))
+        if U % 2 == 0:
+            w.open("if (%s + %d <= nnz)" % (q, U))
+            for u in range(0, U, 2):
+                w("{ const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + %s + %d));"
+                  " ci[%d] = a.x; ci[%d] = a.y; }" % (q, u, u, u + 1))
+                w("{ const tg_f64x2 b = __builtin_nontemporal_load((const tg_f64x2*)(data + %s + %d));"
+                  " cv[%d] = b.x; cv[%d] = b.y; }" % (q, u, u, u + 1))
+            w.close()
+            w.open("else")
+        else:
+            w.open("")
+        for u in range(U):
+            w("ci[%d] = %s + %d < nnz ? __builtin_nontemporal_load(indices + %s + %d) : 0;"
+              % (u, q, u, q, u))
+            w("cv[%d] = %s + %d < nnz ? __builtin_nontemporal_load(data + %s + %d) : 0.0;"
+              % (u, q, u, q, u))
+        w.close()
+        w("double xv[%d];" % U)
+        w("#pragma unroll")
+        w.open("for (int u = 0; u < %d; ++u)" % U)
+        w("const tg_i64 pu = %s + u;" % q)
+        w("const bool in_row = pu >= rs[%s] && pu < re[%s];" % (r, r))
+        w("cv[u] = in_row ? cv[u] : 0.0;")
+        w("ci[u] = in_row ? ci[u] : 0;")
+        w("xv[u] = %s;" % _cexpr(_gather_operand(plan), _Env({row: "row", col: "ci[u]"},
+                                                              p="pu")))
+        w.close()
+        w("#pragma unroll")
+        w.open("for (int u = 0; u < %d; ++u)" % U)
+        w("acc[%s] += %s;" % (r, _value_with(plan, "cv[u]", "xv[u]", row, "ci[u]")))
+        w.close()
+
+    w("// first step of every row in flight before any accumulation")
+    w("#pragma unroll")
+    w.open("for (int r = 0; r < %d; ++r)" % R)
+    w("const tg_i64 row = row0 + slot + r * %d;" % SLOTS)
+    w("(void)row;")
+    w("const tg_i64 q = (rs[r] & ~(tg_i64)%d) + (tg_i64)lane * %d;" % (ALIGN - 1, U))
+    w.open("if (q < re[r] && rs[r] < re[r])")
+    step("q", "r")
+    w.close()
+    w.close()
+    w("// remaining steps (rows longer than %d nonzeros)" % (STEP - ALIGN + 1))
+    w("#pragma unroll")
+    w.open("for (int r = 0; r < %d; ++r)" % R)
+    w("const tg_i64 row = row0 + slot + r * %d;" % SLOTS)
+    w("(void)row;")
+    w("#pragma unroll 1")
+    w.open("for (tg_i64 q = (rs[r] & ~(tg_i64)%d) + (tg_i64)lane * %d + %d; q < re[r]; q += %d)"
+           % (ALIGN - 1, U, STEP, STEP))
+    step("q", "r")
+    w.close()
+    w.close()
+    w("#pragma unroll")
+    w.open("for (int r = 0; r < %d; ++r)" % R)
+    if TPR > 1:
+        w("acc[r] = tg_segsum<%d>(acc[r]);" % TPR)
+    w("const int lr = slot + r * %d;" % SLOTS)
+    w("const tg_i64 row = row0 + lr;")
+    w.open("if (%slr < %d && row < row_end)" % ("lane == 0 && " if TPR > 1 else "", TR))
+    env = _Env({row: "row"}, acc="acc[r]")
+    w("%s[%s] = %s;" % (out_name, _offset(plan.out_tensor, plan.out.indices, env),
+                         _cexpr(plan.final_expr, env)))
+    w.close()
+    w.close()
+
+
+def _gather_operand(plan: Plan) -> Expr:
+    """The dense factor of the per-nonzero product (``x[j]`` for spmv)."""
+    for n in plan.value_expr.walk():
+        if isinstance(n, Access) and not n.tensor.format.is_sparse() and n.tensor.order > 0:
+            return n
+    raise NotImplementedError("scalar_reduce without a dense gathered operand")
+
+
+def _value_with(plan: Plan, data_text: str, gathered_text: str, row: str, col_text: str) -> str:
+    """value_expr with the sparse value and the gathered operand substituted."""
+    g = _gather_operand(plan)
+
+    def rec(e: Expr) -> str:
+        if e is g:
+            return gathered_text
+        if isinstance(e, Access):
+            if e.tensor.format.is_sparse():
+                return data_text
+            return _cexpr(e, _Env({row: "row", plan.col_idx.name: col_text}, p="pu"))
+        if isinstance(e, Const):
+            return _fmt_const(e.value)
+        if isinstance(e, Mul):
+            return "(%s * %s)" % (rec(e.left), rec(e.right))
+        if isinstance(e, Add):
+            return "(%s + %s)" % (rec(e.left), rec(e.right))
+        raise TypeError("cannot emit %r" % (e,))
+    return rec(plan.value_expr)
+
+
+def _hip_row_dense_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeometry,
+                       out_name: str, b_name: str, kext: str) -> None:
+    """C[row, :] = sum over nonzeros data[p] * B[col, :]; written once."""
+    B, TPR = geo.block, max(1, low.threads_per_row)
+    U = max(1, low.unroll)
+    V = 2 if low.vector_width >= 2 else 1
+    SLOTS = B // TPR
+    TR = geo.rows_per_block
+    R = (TR + SLOTS - 1) // SLOTS
+    uniform = TPR == WAVE
+    w("const tg_i64 row_end = %s;" % bound)
+    w("const tg_i64 row0 = (tg_i64)blockIdx.x * %d;" % TR)
+    w("const int lane = threadIdx.x %% %d;" % TPR)
+    if uniform:
+        w("// a whole wave per row: row bounds and (column, value) pairs are wave-uniform")
+        w("const int slot = __builtin_amdgcn_readfirstlane(threadIdx.x / %d);" % TPR)
+    else:
+        w("const int slot = threadIdx.x / %d;" % TPR)
+    if V == 2:
+        w("const bool vec_ok = ((%s & 1) == 0) && ((((unsigned long long)%s) | "
+          "((unsigned long long)%s)) & 15) == 0;" % (kext, b_name, out_name))
+    w("#pragma unroll 1")
+    w.open("for (int r = 0; r < %d; ++r)" % R)
+    w("const int lr = slot + r * %d;" % SLOTS)
+    w("const tg_i64 row = row0 + lr;")
+    w("if (lr >= %d || row >= row_end) break;" % TR)
+    if uniform:
+        w("const tg_i64 rs = tg_uniform(indptr[row]);")
+        w("const tg_i64 re = tg_uniform(indptr[row + 1]);")
+    else:
+        w("const tg_i64 rs = indptr[row];")
+        w("const tg_i64 re = indptr[row + 1];")
+
+    def kloop(vec: bool) -> None:
+        width = 2 if vec else 1
+        w("#pragma unroll 1")
+        w.open("for (tg_i64 k0 = (tg_i64)lane * %d; k0 < %s; k0 += %d)" % (width, kext, TPR * width))
+        w("double a0 = 0.0%s;" % (", a1 = 0.0" if vec else ""))
+        w("tg_i64 p = rs;")
+        w("#pragma unroll 1")
+        w.open("for (; p + %d <= re; p += %d)" % (U, U))
+        w("tg_i64 j[%d]; double v[%d];" % (U, U))
+        w("#pragma unroll")
+        w.open("for (int u = 0; u < %d; ++u)" % U)
+        w("j[u] = indices[p + u]; v[u] = data[p + u];")
+        w.close()
+        if vec:
+            w("tg_f64x2 b[%d];" % U)
+            w("#pragma unroll")
+            w.open("for (int u = 0; u < %d; ++u)" % U)
+            w("b[u] = *(const tg_f64x2*)(%s + j[u] * %s + k0);" % (b_name, kext))
+            w.close()
+            w("#pragma unroll")
+            w.open("for (int u = 0; u < %d; ++u)" % U)
+            w("a0 += v[u] * b[u].x; a1 += v[u] * b[u].y;")
+            w.close()
+        else:
+            w("double b[%d];" % U)
+            w("#pragma unroll")
+            w.open("for (int u = 0; u < %d; ++u)" % U)
+            w("b[u] = %s[j[u] * %s + k0];" % (b_name, kext))
+            w.close()
+            w("#pragma unroll")
+            w.open("for (int u = 0; u < %d; ++u)" % U)
+            w("a0 += v[u] * b[u];")
+            w.close()
+        w.close()
+        w.open("for (; p < re; ++p)")
+        w("const tg_i64 jj = indices[p]; const double vv = data[p];")
+        if vec:
+            w("const tg_f64x2 bb = *(const tg_f64x2*)(%s + jj * %s + k0);" % (b_name, kext))
+            w("a0 += vv * bb.x; a1 += vv * bb.y;")
+        else:
+            w("a0 += vv * %s[jj * %s + k0];" % (b_name, kext))
+        w.close()
+        if vec:
+            w("tg_f64x2 c; c.x = a0; c.y = a1;")
+            w("*(tg_f64x2*)(%s + row * %s + k0) = c;" % (out_name, kext))
+        else:
+            w("%s[row * %s + k0] = a0;" % (out_name, kext))
+        w.close()
+
+    if V == 2:
+        w.open("if (vec_ok)")
+        kloop(True)
+        w.close()
+        w.open("else")
+        kloop(False)
+        w.close()
+    else:
+        kloop(False)
+    w.close()
+
+
+def _hip_sparse_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeometry,
+                    out_name: str, u_name: str, v_name: str, kext: str) -> None:
+    """out[p] = data[p] * dot(U[row, :], V[col, :]) over the row's nonzeros."""
+    B, TPR = geo.block, max(1, low.threads_per_row)
+    U = max(1, low.unroll)
+    V = 2 if low.vector_width >= 2 else 1
+    WAVES = B // WAVE
+    SLOTS = WAVE // TPR
+    TR = geo.rows_per_block
+    R = (TR + WAVES - 1) // WAVES
+    w("const tg_i64 row_end = %s;" % bound)
+    w("const tg_i64 row0 = (tg_i64)blockIdx.x * %d;" % TR)
+    w("const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / %d);" % WAVE)
+    w("const int wl = threadIdx.x %% %d;" % WAVE)
+    w("const int kq = wl %% %d;      // lane within one nonzero's group" % TPR)
+    w("const int slot = wl / %d;     // which nonzero of the pass" % TPR)
+    if V == 2:
+        w("const bool vec_ok = ((%s & 1) == 0) && ((((unsigned long long)%s) | "
+          "((unsigned long long)%s)) & 15) == 0;" % (kext, u_name, v_name))
+    w("#pragma unroll 1")
+    w.open("for (int r = 0; r < %d; ++r)" % R)
+    w("const int lr = wave + r * %d;" % WAVES)
+    w("const tg_i64 row = row0 + lr;")
+    w("if (lr >= %d || row >= row_end) break;" % TR)
+    w("const tg_i64 rs = tg_uniform(indptr[row]);")
+    w("const tg_i64 re = tg_uniform(indptr[row + 1]);")
+    w("const double* __restrict__ urow = %s + row * %s;" % (u_name, kext))
+    w("#pragma unroll 1")
+    w.open("for (tg_i64 p0 = rs; p0 < re; p0 += %d)" % SLOTS)
+    w("const tg_i64 p = p0 + slot;")
+    w("const bool valid = p < re;")
+    w("double acc = 0.0;")
+    w.open("if (valid)")
+    w("const double* __restrict__ vrow = %s + indices[p] * %s;" % (v_name, kext))
+
+    def kloop(vec: bool) -> None:
+        width = 2 if vec else 1
+        chunk = TPR * width
+        w("tg_i64 k = (tg_i64)kq * %d;" % width)
+        w("#pragma unroll 1")
+        w.open("for (; k + %d <= %s; k += %d)" % (chunk * (U - 1) + width, kext, chunk * U))
+        if vec:
+            w("tg_f64x2 a[%d], b[%d];" % (U, U))
+            w("#pragma unroll")
+            w.open("for (int u = 0; u < %d; ++u)" % U)
+            w("a[u] = *(const tg_f64x2*)(urow + k + u * %d);" % chunk)
+            w("b[u] = *(const tg_f64x2*)(vrow + k + u * %d);" % chunk)
+            w.close()
+            w("#pragma unroll")
+            w.open("for (int u = 0; u < %d; ++u)" % U)
+            w("acc += a[u].x * b[u].x; acc += a[u].y * b[u].y;")
+            w.close()
+        else:
+            w("double a[%d], b[%d];" % (U, U))
+            w("#pragma unroll")
+            w.open("for (int u = 0; u < %d; ++u)" % U)
+            w("a[u] = urow[k + u * %d]; b[u] = vrow[k + u * %d];" % (chunk, chunk))
+            w.close()
+            w("#pragma unroll")
+            w.open("for (int u = 0; u < %d; ++u)" % U)
+            w("acc += a[u] * b[u];")
+            w.close()
+        w.close()
+        w("#pragma unroll 1")
+        w.open("for (; k < %s; k += %d)" % (kext, chunk))
+        if vec:
+            w("const tg_f64x2 a = *(const tg_f64x2*)(urow + k);")
+            w("const tg_f64x2 b = *(const tg_f64x2*)(vrow + k);")
+            w("acc += a.x * b.x; acc += a.y * b.y;")
+        else:
+            w("acc += urow[k] * vrow[k];")
+        w.close()
+
+    if V == 2:
+        w.open("if (vec_ok)")
+        kloop(True)
+        w.close()
+        w.open("else")
+        kloop(False)
+        w.close()
+    else:
+        kloop(False)
+    w.close()
+    if TPR > 1:
+        w("acc = tg_segsum<%d>(acc);" % TPR)
+    env = _Env({plan.row_idx.name: "row"}, p="p", acc="acc")
+    w.open("if (valid%s)" % (" && kq == 0" if TPR > 1 else ""))
+    w("%s[p] = %s;" % (out_name, _cexpr(plan.final_expr, env)))
+    w.close()
+    w.close()
+    w.close()
+
+
+def _hip_elementwise(w: _W, plan: Plan, bound: str, geo: LaunchGeometry, out_name: str) -> None:
+    ix = plan.out.indices[0]
+    w("const tg_i64 i = (tg_i64)blockIdx.x * %d + threadIdx.x;" % geo.block)
+    w("if (i >= %s) return;" % bound)
+    env = _Env({ix.name: "i"})
+    w("%s[%s] = %s;" % (out_name, _offset(plan.out_tensor, plan.out.indices, env),
+                        _cexpr(plan.value_expr, env)))
+
+
+def _dense_name(plan: Plan, which: int) -> str:
+    dense = []
+    for n in plan.value_expr.walk():
+        if (isinstance(n, Access) and not n.tensor.format.is_sparse() and n.tensor.order > 0
+                and n.tensor.name not in dense):
+            dense.append(n.tensor.name)
+    return dense[which]
+
+
+def _hip_kernel_text(kernel: Kernel, config: Config, plan: Plan, low: Lowering,
+                     args: List[Tuple[str, str]], geo: LaunchGeometry) -> str:
+    bound = "(%s - 1)" % plan.row_extent if config.inject_bug else plan.row_extent
+    out_name = plan.out_tensor.name
+    w = _W()
+    w("extern \"C\" __global__ __launch_bounds__(%d)" % geo.block)
+    w.open("void %s_kernel(%s)" % (kernel.name, _hip_decls(args)))
+    if plan.kind == "scalar_reduce":
+        if not plan.reduce_is_compressed:
+            raise NotImplementedError("HIP scalar_reduce needs the reduction over the "
+                                      "compressed index")
+        _hip_scalar_reduce(w, plan, low, bound, geo, out_name)
+    elif plan.kind == "row_dense_out":
+        kext = _extent_for(plan, plan.inner_out[0].name)
+        _hip_row_dense_out(w, plan, low, bound, geo, out_name, _dense_name(plan, 0), kext)
+    elif plan.kind == "sparse_out":
+        kext = _extent_for(plan, plan.reduce.index.name)
+        _hip_sparse_out(w, plan, low, bound, geo, out_name, _dense_name(plan, 0),
+                        _dense_name(plan, 1), kext)
+    elif plan.kind == "elementwise":
+        _hip_elementwise(w, plan, bound, geo, out_name)
+    else:  # pragma: no cover
+        raise NotImplementedError(plan.kind)
+    w.close()
+    return w.text()
+
+
+def emit_hip(kernel: Kernel, config: Config) -> str:
+    """Device translation unit of a lowered kernel (hipRTC input)."""
+    plan, low = _plan(kernel), _lowering(kernel)
+    _check_hip_schedule(plan, low)
+    _sig, args, _info = abi_of(kernel)
+    geo = launch_geometry(plan, low)
+    extra = ["target      : %s (wave%d)" % (HIP_ARCH, WAVE),
+             "launch      : grid = ceil(%s / %d), block = %d, lds = %d B"
+             % (geo.rows_symbol, geo.rows_per_block, geo.block, geo.lds_bytes)]
+    return "\n".join([_header(kernel, config, "hip", low, extra), _HIP_PRELUDE.strip(), "",
+                      _hip_kernel_text(kernel, config, plan, low, args, geo), ""])
+
+
+def emit_hip_host(kernel: Kernel, config: Config) -> str:
+    """C launcher for a HIP variant.
+
+    ``{CODE_OBJECT}`` and ``{CODE_SIZE}`` are replaced by the compiled bytes
+    when the variant is built.  The launcher exports the reference ABI
+    (synchronous, device pointers, errors reported through ``tg_last_error``)
+    plus ``tgv_geometry``, ``tgv_function`` and ``tgv_launch_async`` for
+    harnesses that time the kernel on their own stream.
+    """
+    plan, low = _plan(kernel), _lowering(kernel)
+    sig, args, _info = abi_of(kernel)
+    geo = launch_geometry(plan, low)
+    sym = "%s_kernel" % kernel.name
+    names = [n for _t, n in args]
+    dims = {n for t, n in args if t == "int64_t"}
+    rows = geo.rows_symbol
+    pack = []
+    for ct, n in args:
+        if ct.endswith("*"):
+            pack.append("  a[%d] = (uint64_t)(uintptr_t)%s;" % (len(pack), n))
+        elif ct in ("double", "float"):
+            pack.append("  memcpy(&a[%d], &%s, sizeof(double));" % (len(pack), n))
+        else:
+            pack.append("  a[%d] = (uint64_t)%s;" % (len(pack), n))
+    kdim = "K" if "K" in dims else "0"
+    ndim = "N" if "N" in dims else "0"
+    nnz = "nnz" if "nnz" in dims else "0"
+    params = ", ".join("%s %s" % a for a in args)
+    text = """/* TileGen HIP launcher for %(sym)s -- generated, DO NOT EDIT.
+ * schedule %(sched)s; grid = ceil(%(rows)s / %(rpb)d), block = %(block)d, lds = %(lds)d B */
+#include <stdint.h>
+#include <string.h>
+#include "tgrt.h"
+
+static const unsigned char tg_code[{CODE_SIZE}] = {{CODE_OBJECT}};
+
+void* tgv_function(void) {
+  tg_function fn = 0;
+  if (tg_code_function(tg_code, sizeof(tg_code), "%(sym)s", &fn) != 0) return 0;
+  return fn;
+}
+
+const char* tgv_kernel_name(void) { return "%(name)s"; }
+
+int tgv_geometry(int64_t M, int64_t N, int64_t K, int64_t nnz,
+                 int64_t* grid, int32_t* block, int32_t* lds) {
+  (void)N; (void)K; (void)nnz;
+  const int64_t rows = %(rows_expr)s;
+  *grid = rows > 0 ? (rows + %(rpb)d - 1) / %(rpb)d : 0;
+  *block = %(block)d;
+  *lds = %(lds)d;
+  return 0;
+}
+
+static int tgv_pack(uint64_t* a, %(params)s) {
+%(pack)s
+  return %(nargs)d;
+}
+
+int tgv_launch_async(void* stream, %(params)s) {
+  tg_function fn = (tg_function)tgv_function();
+  if (!fn) return tg_last_status();
+  int64_t grid; int32_t block, lds;
+  tgv_geometry(%(M)s, %(N)s, %(K)s, %(nnz)s, &grid, &block, &lds);
+  if (grid == 0) return 0;
+  uint64_t a[%(nargs)d];
+  int n = tgv_pack(a, %(names)s);
+  return tg_launch(fn, grid, block, lds, a, n, stream, 0);
+}
+
+%(sig)s {
+  tg_clear_error();
+  if (tgv_launch_async(0, %(names)s) == 0) tg_synchronize();
+}
+""" % {
+        "sym": sym, "name": kernel.name, "sched": config.short(), "rows": rows,
+        "rpb": geo.rows_per_block, "block": geo.block, "lds": geo.lds_bytes,
+        "rows_expr": rows if rows in dims else "M", "params": params,
+        "pack": "\n".join(pack), "nargs": len(args), "names": ", ".join(names),
+        "sig": sig, "M": "M" if "M" in dims else "0", "N": ndim, "K": kdim, "nnz": nnz,
+    }
+    return text
+
+
+# --------------------------------------------------------------------------- #
+# public entry point
+# --------------------------------------------------------------------------- #
+def generate(kernel: Kernel, config: Config, backend: str = "cpu",
+             outdir: Optional[str] = "build/generated", write: bool = True,
+             skip_passes: Sequence[str] = ()) -> GeneratedKernel:
+    """Run the pass pipeline and emit source for ``backend`` ("hip" or "cpu")."""
+    if backend not in ("hip", "cpu"):
+        raise ValueError("backend must be 'hip' or 'cpu', got %r" % backend)
+    optimized = _passes.run_pipeline(kernel, config, backend=backend, skip=skip_passes)
+    sig, args, _info = abi_of(optimized)
+    if backend == "hip":
+        source, ext = emit_hip(optimized, config), "hip"
+        host = emit_hip_host(optimized, config)
+        plan, low = _plan(optimized), _lowering(optimized)
+        geo = launch_geometry(plan, low)
+        sym = "%s_kernel" % optimized.name
+    else:
+        source, ext, host, geo, sym = emit_cpu(optimized, config), "cpp", "", None, ""
+    digest = hashlib.sha1((source + host).encode()).hexdigest()[:8]
+    gen = GeneratedKernel(
+        source=source, filename="%s_%s_%s.%s" % (optimized.name, config.hash(), digest, ext),
+        abi_signature=sig, pass_log=optimized.pass_log, backend=backend,
+        kernel_name=optimized.name, config=config, host_source=host, device_symbol=sym,
+        geometry=geo, abi_args=args)
+    if write and outdir:
+        gen.write(outdir)
+    return gen

@@ -1,0 +1,52 @@
+"""Named schedules: the tuned default per BASELINE case and the fixed set the
+GPU parity tests sweep.
+
+``TUNED`` holds the schedule each BASELINE case runs with unless a caller
+passes its own (``bench.py --config``); values come from the CDNA4 search in
+``autotune`` on an MI355X and are re-checked whenever the kernels change.
+"""
+
+from __future__ import annotations
+
+from typing import Dict, List
+
+from .codegen import Config
+
+TUNED: Dict[str, Config] = {
+    # 16 nonzeros per row: 8 lanes x 2 consecutive nonzeros (one 128-bit load of
+    # indices and one of values per lane), 8 rows per wave, 4 rows per lane group
+    "c1": Config(tile_size=128, threads_per_row=8, unroll=2, vector_width=1, block_size=256),
+    # 7 nonzeros per row: 4 lanes x 2
+    "c2": Config(tile_size=256, threads_per_row=4, unroll=2, vector_width=1, block_size=256),
+    "c3a": Config(tile_size=64, threads_per_row=8, unroll=2, vector_width=1, block_size=256),
+    "c3b": Config(tile_size=32, threads_per_row=16, unroll=4, vector_width=1, block_size=256),
+    # K = 64: 32 lanes x 2 columns per row, 2 rows per wave, 4 nonzeros in flight
+    "c4": Config(tile_size=8, threads_per_row=32, unroll=4, vector_width=2, block_size=256),
+    # 16 nonzeros per row, K = 64: 4 lanes per nonzero x 2 columns per load
+    "c5": Config(tile_size=4, threads_per_row=4, unroll=2, vector_width=2, block_size=256),
+    "c5x25": Config(tile_size=4, threads_per_row=4, unroll=2, vector_width=2, block_size=256),
+}
+
+# Swept by the GPU parity tests for every kernel: every threads_per_row the
+# wave allows, tiles below/at/above the lane-group count, unroll 1..8, both
+# vector widths, and an untiled schedule (reference tests/test_cuda_gpu.py:34-44
+# covers the same dimensions for its CUDA emitter).
+TEST_SCHEDULES: List[Config] = [
+    Config(tile_size=32, threads_per_row=1, unroll=1, vector_width=1, block_size=128),
+    Config(tile_size=64, threads_per_row=2, unroll=2, vector_width=1, block_size=128),
+    Config(tile_size=64, threads_per_row=4, unroll=4, vector_width=2, block_size=256),
+    Config(tile_size=128, threads_per_row=8, unroll=2, vector_width=2, block_size=512),
+    Config(tile_size=32, threads_per_row=16, unroll=3, vector_width=1, block_size=256),
+    Config(tile_size=16, threads_per_row=32, unroll=8, vector_width=2, block_size=512),
+    Config(tile_size=4, threads_per_row=64, unroll=4, vector_width=1, block_size=256),
+    Config(tile_size=1, threads_per_row=4, unroll=1, vector_width=1, block_size=64),
+    Config(tile_size=256, threads_per_row=1, unroll=4, vector_width=1, block_size=256),
+    Config(tile_size=1024, threads_per_row=8, unroll=2, vector_width=2, block_size=1024),
+]
+
+TEST_KERNELS = ["spmv", "spmm", "sddmm", "fused_spmv_axpy", "axpy"]
+
+
+def schedule_id(c: Config) -> str:
+    return "T%d-TPR%d-U%d-V%d-B%d" % (c.tile_size, c.threads_per_row, c.unroll,
+                                      c.vector_width, c.block_size)
