@@ -70,6 +70,40 @@ def _traffic(kernel: str, case_id: str):
     return d.get("hbm_bytes_per_launch")
 
 
+_COPY_SRC = r"""
+extern "C" __global__ __launch_bounds__(256)
+void tg_copy_kernel(const double* __restrict__ src, double* __restrict__ dst, long long n) {
+  const long long stride = (long long)gridDim.x * 256;
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
+    dst[i] = src[i];
+}
+"""
+
+
+def calibrate_copy(mib: int, launches: int = 10) -> int:
+    """Launch a plain copy of ``mib`` MiB ``launches`` times, so a rocprofv3
+    --pmc run can relate FETCH_SIZE / WRITE_SIZE to a known byte count."""
+    import ctypes
+    from tilegen_amd import runtime as rt
+    from tilegen_amd.verify import hiprtc_options
+    code, _ = rt.rtc_compile(_COPY_SRC, "tg_copy.hip", hiprtc_options())
+    blob = ctypes.create_string_buffer(code, len(code))
+    mod, fn = ctypes.c_void_p(), ctypes.c_void_p()
+    rt.check(rt.lib().tg_module_load(blob, len(code), ctypes.byref(mod)), "module")
+    rt.check(rt.lib().tg_module_function(mod, b"tg_copy_kernel", ctypes.byref(fn)), "function")
+    n = (mib << 20) // 8
+    src = rt.DeviceBuffer(np.arange(n, dtype=np.float64))
+    dst = rt.DeviceBuffer(nbytes=n * 8)
+    for _ in range(launches):
+        rt.launch(fn.value, 4096, 256, 0, [src, dst, n])
+    ok = bool(np.array_equal(dst.to_host(np.empty(n)), np.arange(n, dtype=np.float64)))
+    print(json.dumps({"calibration": "tg_copy_kernel", "bytes_read": n * 8,
+                      "bytes_written": n * 8, "launches": launches, "ok": ok}), flush=True)
+    src.free()
+    dst.free()
+    return 0 if ok else 1
+
+
 def _cpu_baseline(kernel, A, ops, budget_s: float):
     import oracle
     kind = "reference" if oracle.reference_available() else "port"
@@ -106,12 +140,17 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--warm", action="store_true",
                     help="no input rotation (cache-warm figure, reported as such)")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only launch a plain copy of MIB MiB (PMC byte-count calibration)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1:
         print("bench.py runs on exactly one GPU: this build has no multi-GPU path "
               "(--gpus %d requested). Run with --gpus 1." % args.gpus, file=sys.stderr)
         return 2
+
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy)
 
     from tilegen_amd import runtime as rt
     from tilegen_amd.matrices import (baseline_case, baseline_operands, compulsory_bytes,

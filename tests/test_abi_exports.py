@@ -1,0 +1,102 @@
+"""The C ABI: every function include/*.h declares is exported by the library
+that provides it (libtgrt.so for tgrt.h, each generated variant library for
+tilegen_launch.h), and the libraries load without a GPU.  No compute calls."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from tilegen_amd import runtime
+from tilegen_amd.codegen import Config, generate
+from tilegen_amd.dsl import standard_kernels
+from tilegen_amd.verify import compile_generated
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared(header: str):
+    text = open(os.path.join(ROOT, "include", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tg_[a-z_0-9]+|tgv_[a-z_0-9]+|launch_[a-z_0-9]+)\s*\(",
+                                 text)))
+
+
+def _exported(path: str):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True,
+                         check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if " T " in line}
+
+
+def test_runtime_exports_every_declared_symbol():
+    declared = _declared("tgrt.h")
+    assert len(declared) >= 25
+    exported = _exported(runtime.lib_path())
+    missing = [s for s in declared if s not in exported]
+    assert not missing, missing
+    L = runtime.lib()  # loads without a GPU
+    for s in declared:
+        assert hasattr(L, s)
+
+
+@pytest.mark.parametrize("kernel", ["spmv", "spmm", "sddmm"])
+def test_variant_library_exports_launch_abi(kernel, tmp_path):
+    gen = generate(standard_kernels()[kernel], Config(tile_size=64, threads_per_row=8,
+                                                      unroll=2, block_size=256),
+                   "hip", outdir=str(tmp_path))
+    so, log = compile_generated(gen, "hip", str(tmp_path))
+    declared = [s for s in _declared("tilegen_launch.h")
+                if not s.startswith("launch_") or s == "launch_%s" % kernel]
+    exported = _exported(so)
+    assert not [s for s in declared if s not in exported]
+    runtime.lib()
+    lib = ctypes.CDLL(so)
+    lib.tgv_kernel_name.restype = ctypes.c_char_p
+    assert lib.tgv_kernel_name().decode() == kernel
+    g, b, l = ctypes.c_int64(), ctypes.c_int32(), ctypes.c_int32()
+    lib.tgv_geometry.argtypes = [ctypes.c_int64] * 4 + [ctypes.c_void_p] * 3
+    assert lib.tgv_geometry(1000, 1000, 64, 5000, ctypes.byref(g), ctypes.byref(b),
+                            ctypes.byref(l)) == 0
+    assert b.value == 256 and g.value * 64 >= 1000 if kernel != "sddmm" else g.value > 0
+
+
+def test_runtime_error_reporting_without_device():
+    L = runtime.lib()
+    L.tg_clear_error()
+    assert L.tg_last_status() == 0 and runtime.last_error() == ""
+    with pytest.raises(runtime.TileGenHipError):
+        runtime.check(L.tg_launch(None, 1, 64, 0, None, 0, None, 1), "launch")
+    assert "null function" in runtime.last_error()
+
+
+def test_rtc_compile_and_errors():
+    code, _ = runtime.rtc_compile('extern "C" __global__ void k(double* a) { a[0] = 1.0; }',
+                                  "k.hip", ["--offload-arch=gfx950", "-O3"])
+    assert code[:4] == b"\x7fELF"
+    with pytest.raises(runtime.TileGenHipError) as err:
+        runtime.rtc_compile("this is not HIP", "bad.hip", ["--offload-arch=gfx950"])
+    assert "bad.hip" in str(err.value)
+
+
+def test_no_packed_fp32_in_generated_code(tmp_path):
+    """Generated kernels are compiled without packed-FP32 operations."""
+    objdump = "/opt/rocm/llvm/bin/llvm-objdump"
+    if not os.path.exists(objdump):
+        pytest.skip("llvm-objdump not available")
+    from tilegen_amd.verify import cache_dir
+    for kernel in ("spmv", "spmm", "sddmm"):
+        gen = generate(standard_kernels()[kernel], Config(tile_size=64, threads_per_row=8,
+                                                          unroll=2, vector_width=2,
+                                                          block_size=256),
+                       "hip", outdir=str(tmp_path))
+        so, _ = compile_generated(gen, "hip", str(tmp_path))
+        co = so[:-3] + ".co"
+        asm = subprocess.run([objdump, "-d", "--mcpu=gfx950", co], capture_output=True,
+                             text=True).stdout
+        assert "v_pk_fma_f32" not in asm and "v_pk_add_f32" not in asm and \
+            "v_pk_mul_f32" not in asm
+        assert "scratch_" not in asm  # no register spills

@@ -1,0 +1,282 @@
+"""Pass pipeline and emitters (reference tests/test_passes.py:24-158 and the
+emitter checks of tests/test_verify.py:53-89), for the HIP and CPU backends.
+No GPU: HIP sources are checked as text and compiled by hipRTC for gfx950."""
+
+from __future__ import annotations
+
+import os
+
+import pytest
+
+from tilegen_amd import passes
+from tilegen_amd.codegen import (Config, abi_of, emit_cpu, emit_hip, emit_hip_host,
+                                 generate, launch_geometry, _lowering, _plan)
+from tilegen_amd.dsl import (CSR, Index, assign, dense_tensor, kernel, reduce_sum,
+                             scalar_tensor, sparse_tensor, standard_kernels)
+
+
+def _run(k, cfg=None, backend="cpu", skip=()):
+    return passes.run_pipeline(k, cfg or Config(), backend=backend, skip=skip)
+
+
+def _code(src: str) -> str:
+    return "\n".join(l for l in src.splitlines() if not l.lstrip().startswith("//"))
+
+
+def test_pass_names_and_order():
+    assert passes.PASS_NAMES == ["canonicalize", "loop_fusion", "tiling", "thread_mapping",
+                                 "unroll", "vectorize", "dead_code_elim"]
+    assert passes.optimize is passes.run_pipeline
+
+
+def test_fusion_collapses_two_loop_nests():
+    out = _run(standard_kernels()["fused_spmv_axpy"])
+    assert len(out.stmts) == 1
+    fusion = [e for e in out.pass_log if e["pass"] == "loop_fusion"]
+    assert fusion and "fused" in fusion[0]["action"]
+    reads = [n.tensor.name for st in out.stmts for n in st.rhs.walk() if hasattr(n, "tensor")]
+    assert "t" not in reads
+
+
+def test_fusion_refused_on_true_dependency():
+    i, j, kk = Index("i"), Index("j"), Index("kk")
+    A = sparse_tensor("A", CSR, shape=("M", "N"))
+    x = dense_tensor("x", shape=("N",))
+    w = dense_tensor("w", shape=("M",))
+    t = dense_tensor("t", shape=("M",))
+    z = dense_tensor("z", shape=("M",))
+    alpha, beta = scalar_tensor("alpha"), scalar_tensor("beta")
+    k = kernel("dependent", [assign(t[i], reduce_sum(j, A[i, j] * x[j])),
+                             assign(z[kk], alpha * t[kk] + beta * w[kk])])
+    out = _run(k)
+    assert len(out.stmts) == 2
+    fusion = [e for e in out.pass_log if e["pass"] == "loop_fusion"]
+    assert fusion and "refused" in fusion[0]["action"]
+
+
+def test_canonicalize_folds_and_reports_no_change_second_time():
+    i = Index("i")
+    x = dense_tensor("x", shape=("M",))
+    z = dense_tensor("z", shape=("M",))
+    k = kernel("c", [assign(z[i], (1.0 * x[i]) + (2.0 + 3.0) * 0.0 + 0.0)])
+    once = passes.canonicalize(k)
+    assert "no change" not in once.pass_log[-1]["action"]
+    twice = passes.canonicalize(once)
+    assert "no change" in twice.pass_log[-1]["action"]
+    k2 = standard_kernels()["spmv"]
+    assert "no change" in passes.canonicalize(passes.canonicalize(k2)).pass_log[-1]["action"]
+
+
+def test_dead_code_elim_drops_unread_temporary():
+    i, j = Index("i"), Index("j")
+    A = sparse_tensor("A", CSR, shape=("M", "N"))
+    x = dense_tensor("x", shape=("N",))
+    y = dense_tensor("y", shape=("M",))
+    t = dense_tensor("t", shape=("M",))
+    k = kernel("dce", [assign(y[i], reduce_sum(j, A[i, j] * x[j])), assign(t[i], x[i] * 2.0)])
+    out = passes.dead_code_elim(k)
+    assert "removed 0" in out.pass_log[-1]["action"]  # both are outputs
+
+
+def test_lowering_transforms_recorded_in_schedule():
+    cfg = Config(tile_size=64, threads_per_row=8, unroll=4, vector_width=2, block_size=512)
+    spmm = _run(standard_kernels()["spmm"], cfg, "hip")
+    low = _lowering(spmm)
+    assert (low.tile, low.threads_per_row, low.unroll, low.vector_width, low.block_size) == \
+        (64, 8, 4, 2, 512)
+    assert low.tiled and low.parallel
+    spmv = _run(standard_kernels()["spmv"], cfg, "hip")
+    assert _lowering(spmv).vector_width == 1  # the spmv gather is not vectorized
+    vec = [e for e in spmv.pass_log if e["pass"] == "vectorize"][0]
+    assert "skipped" in vec["action"]
+    tm = [e for e in spmv.pass_log if e["pass"] == "thread_mapping"][0]
+    assert "wave64" in tm["action"] and "8 lanes per row" in tm["action"]
+
+
+def test_pipeline_idempotent_on_canonical_ir():
+    cfg = Config(tile_size=64, unroll=2, threads_per_row=4)
+    for name in ("spmv", "spmm", "sddmm", "fused_spmv_axpy"):
+        once = _run(standard_kernels()[name], cfg, "hip")
+        twice = _run(once, cfg, "hip")
+        d1, d2 = once.to_dict(), twice.to_dict()
+        d1.pop("pass_log")
+        d2.pop("pass_log")
+        assert d1 == d2, name
+
+
+# --------------------------------------------------------------------------- #
+# ABI
+# --------------------------------------------------------------------------- #
+EXPECTED_ABI = {
+    # reference verify.py:166-173 / tilegen_launch.h
+    "spmv": "void launch_spmv(const int64_t* indptr, const int64_t* indices, const double* data, "
+            "const double* x, double* y, int64_t M, int64_t N, int64_t nnz)",
+    "spmm": "void launch_spmm(const int64_t* indptr, const int64_t* indices, const double* data, "
+            "const double* B, double* C, int64_t M, int64_t N, int64_t K, int64_t nnz)",
+    "sddmm": "void launch_sddmm(const int64_t* indptr, const int64_t* indices, "
+             "const double* data, const double* U, const double* V, double* C, int64_t M, "
+             "int64_t N, int64_t K, int64_t nnz)",
+    "fused_spmv_axpy": "void launch_fused_spmv_axpy(const int64_t* indptr, "
+                       "const int64_t* indices, const double* data, const double* x, "
+                       "const double* w, double* z, double alpha, double beta, int64_t M, "
+                       "int64_t N, int64_t nnz)",
+    "axpy": "void launch_axpy(const double* x, const double* w, double* z, double alpha, "
+            "double beta, int64_t M)",
+}
+
+
+@pytest.mark.parametrize("name", sorted(EXPECTED_ABI))
+def test_abi_signature_matches_reference(name):
+    k = _run(standard_kernels()[name], Config(), "hip")
+    sig, _args, _info = abi_of(k)
+    assert sig == EXPECTED_ABI[name]
+
+
+def test_abi_matches_header():
+    here = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    text = " ".join(open(os.path.join(here, "include", "tilegen_launch.h")).read().split())
+    for name in ("spmv", "spmm", "sddmm"):
+        assert " ".join(EXPECTED_ABI[name].split()) in text.replace("( ", "(").replace(
+            "void launch_%s(" % name, "void launch_%s(" % name)
+
+
+# --------------------------------------------------------------------------- #
+# HIP emitter structure
+# --------------------------------------------------------------------------- #
+def _hip(name, cfg, skip=()):
+    return emit_hip(_run(standard_kernels()[name], cfg, "hip", skip), cfg)
+
+
+def test_hip_markers():
+    src = _hip("spmv", Config(tile_size=32, threads_per_row=4, unroll=4, block_size=256))
+    for marker in ('extern "C" __global__', "__launch_bounds__(256)", "spmv_kernel",
+                   "tg_segsum<4>", "#pragma unroll", "__shared__ tg_i64 s_ptr[33]",
+                   "__builtin_nontemporal_load", "tg_i64x2"):
+        assert marker in src, marker
+    assert "__shfl_down_sync" not in src and "cuda" not in src.lower()
+
+
+def test_hip_no_reduction_when_one_lane_per_row():
+    src = _hip("spmv", Config(tile_size=128, threads_per_row=1, unroll=2, block_size=128))
+    assert "tg_segsum<" not in _code(src).split("tg_uniform(tg_i64 v)")[1]
+
+
+def test_skipping_tiling_changes_hip_and_cpu_code():
+    cfg = Config(tile_size=64, threads_per_row=4, unroll=4, block_size=256)
+    k = standard_kernels()["spmv"]
+    assert _code(_hip("spmv", cfg)) != _code(_hip("spmv", cfg, skip=("tiling",)))
+    assert "s_ptr" not in _hip("spmv", cfg, skip=("tiling",))
+    assert _code(emit_cpu(_run(k, cfg), cfg)) != _code(emit_cpu(_run(k, cfg, skip=("tiling",)),
+                                                                cfg))
+
+
+def test_skipping_thread_mapping_changes_hip_code():
+    cfg = Config(tile_size=32, threads_per_row=4, unroll=1, block_size=128)
+    full = _hip("spmv", cfg)
+    ablated = _hip("spmv", cfg, skip=("thread_mapping",))
+    assert "tg_segsum<4>(acc[r])" in full
+    assert "tg_segsum<4>(acc[r])" not in ablated
+    assert _code(full) != _code(ablated)
+
+
+def test_noop_passes_emit_identical_hip_code():
+    cfg = Config(tile_size=32, threads_per_row=1, unroll=1, block_size=256)
+    full = _code(_hip("spmv", cfg))
+    for name in ("canonicalize", "loop_fusion", "vectorize", "dead_code_elim"):
+        assert _code(_hip("spmv", cfg, skip=(name,))) == full, name
+
+
+def test_hip_vectorize_changes_spmm_and_sddmm():
+    for name in ("spmm", "sddmm"):
+        v1 = _hip(name, Config(tile_size=8, threads_per_row=16, unroll=2, vector_width=1,
+                               block_size=256))
+        v2 = _hip(name, Config(tile_size=8, threads_per_row=16, unroll=2, vector_width=2,
+                               block_size=256))
+        assert "vec_ok" in v2 and "tg_f64x2" in _code(v2).split("void %s_kernel" % name)[1]
+        assert "vec_ok" not in v1
+
+
+def test_hip_wave_uniform_spmm_path():
+    src = _hip("spmm", Config(tile_size=4, threads_per_row=64, unroll=4, block_size=256))
+    assert "__builtin_amdgcn_readfirstlane(threadIdx.x / 64)" in src
+    assert "tg_uniform(indptr[row])" in src
+
+
+def test_hip_injected_bug_stops_one_row_short():
+    good = _hip("spmv", Config(tile_size=32, threads_per_row=4, unroll=2))
+    bad = emit_hip(_run(standard_kernels()["spmv"],
+                        Config(tile_size=32, threads_per_row=4, unroll=2, inject_bug=True),
+                        "hip"), Config(tile_size=32, threads_per_row=4, unroll=2,
+                                       inject_bug=True))
+    assert "const tg_i64 row_end = M;" in good
+    assert "const tg_i64 row_end = (M - 1);" in bad
+
+
+def test_launch_geometry_covers_every_row():
+    for cfg, rows_per_block in (
+            (Config(tile_size=32, threads_per_row=4, unroll=4, block_size=256), 32),
+            # tile_size 1 = no Tile transform: one row per lane group
+            (Config(tile_size=1, threads_per_row=4, unroll=1, block_size=128), 32),
+            (Config(tile_size=256, threads_per_row=1, unroll=4, block_size=256), 256)):
+        k = _run(standard_kernels()["spmv"], cfg, "hip")
+        geo = launch_geometry(_plan(k), _lowering(k))
+        assert geo.rows_per_block == rows_per_block
+        assert geo.grid(1000) * geo.rows_per_block >= 1000
+        host = emit_hip_host(k, cfg)
+        assert "(rows + %d - 1) / %d" % (rows_per_block, rows_per_block) in host
+    sd = _run(standard_kernels()["sddmm"], Config(tile_size=8, threads_per_row=4,
+                                                   block_size=256), "hip")
+    assert launch_geometry(_plan(sd), _lowering(sd)).rows_per_block == 8
+    untiled = _run(standard_kernels()["sddmm"], Config(threads_per_row=4, block_size=256),
+                   "hip", skip=("tiling",))
+    assert launch_geometry(_plan(untiled), _lowering(untiled)).rows_per_block == 4
+
+
+@pytest.mark.parametrize("bad", [Config(block_size=96), Config(threads_per_row=3),
+                                 Config(block_size=2048), Config(tile_size=5000),
+                                 Config(unroll=32)])
+def test_hip_rejects_illegal_schedules(bad):
+    with pytest.raises(ValueError):
+        _hip("spmv", bad)
+
+
+def test_generate_names_and_writes(tmp_path):
+    gen = generate(standard_kernels()["sddmm"], Config(), "hip", outdir=str(tmp_path))
+    assert os.path.exists(tmp_path / gen.filename)
+    assert gen.filename.startswith("sddmm_%s_" % Config().hash()) and gen.filename.endswith(".hip")
+    assert gen.abi_signature.startswith("void launch_sddmm")
+    assert "{CODE_OBJECT}" in gen.host_source and "launch_sddmm" in gen.host_source
+    assert gen.device_symbol == "sddmm_kernel"
+    cpu = generate(standard_kernels()["axpy"], Config(), "cpu", outdir=str(tmp_path))
+    assert cpu.filename.endswith(".cpp") and cpu.abi_signature.startswith("void launch_axpy")
+    with pytest.raises(ValueError):
+        generate(standard_kernels()["spmv"], Config(), "cuda", outdir=str(tmp_path))
+
+
+def test_config_hash_closed_form():
+    import hashlib
+    c = Config(tile_size=64, threads_per_row=8, unroll=2, vector_width=1, block_size=128)
+    assert c.hash() == hashlib.sha1(b"64|8|2|1|128|f64|0").hexdigest()[:10]
+    assert Config().hash() != Config(inject_bug=True).hash()
+
+
+# --------------------------------------------------------------------------- #
+# CPU emitter (the OpenMP baseline)
+# --------------------------------------------------------------------------- #
+def test_cpu_tiling_and_unroll_change_source():
+    k = standard_kernels()["spmv"]
+    base = emit_cpu(_run(k, Config(tile_size=1)), Config(tile_size=1))
+    tiled = emit_cpu(_run(k, Config(tile_size=64)), Config(tile_size=64))
+    assert "i_o" not in base and "i_o" in tiled
+    one = emit_cpu(_run(k, Config(unroll=1)), Config(unroll=1))
+    four = emit_cpu(_run(k, Config(unroll=4)), Config(unroll=4))
+    assert four.count("acc += ") > one.count("acc += ")
+    assert "#pragma omp parallel for schedule(dynamic, 256)" in base
+
+
+def test_cpu_simd_pragma_sits_on_its_loop():
+    cfg = Config(tile_size=32, unroll=2, vector_width=2)
+    src = emit_cpu(_run(standard_kernels()["spmm"], cfg), cfg)
+    lines = [l.strip() for l in src.splitlines()]
+    i = lines.index("#pragma omp simd")
+    assert lines[i + 1].startswith("for (")

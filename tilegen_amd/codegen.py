@@ -390,7 +390,7 @@ class _W:
         return self
 
     def open(self, text: str) -> "_W":
-        self(text + " {")
+        self(text + " {" if text else "{")
         self.depth += 1
         return self
 
@@ -512,14 +512,15 @@ def _cpu_body(kernel: Kernel, config: Config, plan: Plan, low: Lowering) -> str:
         def per_nnz(w2: _W, e2: _Env) -> None:
             simd = "#pragma omp simd" if low.vector_width > 1 else None
             if unroll > 1:
-                w2("int64_t ku = 0;")
+                # canonical loop forms, so `omp simd` applies to the main loop
+                w2("const int64_t ku_end = %s - %s %% %d;" % (ext, ext, unroll))
                 if simd:
                     w2(simd)
-                w2.open("for (; ku + %d <= %s; ku += %d)" % (unroll, ext, unroll))
+                w2.open("for (int64_t ku = 0; ku < ku_end; ku += %d)" % unroll)
                 for o in range(unroll):
                     write(w2, e2, "ku + %d" % o)
                 w2.close()
-                w2.open("for (; ku < %s; ++ku)" % ext)
+                w2.open("for (int64_t ku = ku_end; ku < %s; ++ku)" % ext)
                 write(w2, e2, "ku")
                 w2.close()
             else:
