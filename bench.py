@@ -140,6 +140,9 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--warm", action="store_true",
                     help="no input rotation (cache-warm figure, reported as such)")
+    ap.add_argument("--vendor", default=None, metavar="ALG",
+                    help="also time rocSPARSE SpMV (adaptive|rowsplit|lrb|nnzsplit) on the "
+                         "same rotated inputs; reported as an extra field")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only launch a plain copy of MIB MiB (PMC byte-count calibration)")
     args = ap.parse_args(argv)
@@ -230,6 +233,21 @@ def main(argv=None) -> int:
          "events wall %.3f ms/step" % (args.steps, ms_per_step, k_avg_s * 1e6, k_med_s * 1e6,
                                         ev_wall_ms / args.steps))
 
+    vendor = None
+    if args.vendor and case.kernel == "spmv":
+        from tilegen_amd import vendor as vd
+        vsets = [[b["indptr"], b["indices"], b["data"], b["x"], b["y"]] for b in keep]
+        vms, vwall = vd.spmv_time(args.vendor, M, N, nnz, vsets, args.warmup, args.steps)
+        vgot = keep[0]["y"].to_host()
+        verr = float(np.abs(vgot - ref).max() / max(np.abs(ref).max(), 1e-300))
+        vmed = float(np.median(vms)) * 1e-3
+        vendor = {"library": "rocSPARSE", "alg": args.vendor, "us_median": round(vmed * 1e6, 3),
+                  "gbs_median": round(nbytes / vmed / 1e9, 2),
+                  "timer": "hipEvents around each rocsparse_spmv compute call",
+                  "rel_err": verr}
+        _log("rocSPARSE %s: median %.2f us per call (%.0f GB/s), rel err %.2e" % (
+            args.vendor, vmed * 1e6, nbytes / vmed / 1e9, verr))
+
     cpu = None
     if not args.no_cpu:
         kind, sec, iters = _cpu_baseline(case.kernel, A, ops, args.cpu_seconds)
@@ -279,6 +297,7 @@ def main(argv=None) -> int:
             "traffic": _traffic(case.kernel, args.case),
         },
         "cpu_baseline": cpu,
+        "vendor": vendor,
         "check_rel_err": err,
         "device": "%s %s" % (dev["name"], dev["arch"]),
     }

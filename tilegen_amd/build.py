@@ -2,9 +2,10 @@
 
 1. ``tilegen_amd/_lib/libtgrt.so`` (the runtime, include/tgrt.h) with the host
    C++ compiler against the ROCm HIP runtime and hipRTC;
-2. the test oracle (``oracle/Makefile``: the C restatement, and the
+2. ``libtg_vendor.so``, the rocSPARSE comparison (when rocSPARSE is installed);
+3. the test oracle (``oracle/Makefile``: the C restatement, and the
    reference's own ref.cpp where its sources are present);
-3. the hipRTC code objects and C launchers of every named schedule
+4. the hipRTC code objects and C launchers of every named schedule
    (``schedules.TUNED`` and ``TEST_SCHEDULES``) into the kernel cache, so GPU
    runs load prebuilt variants instead of compiling.  hipRTC needs no GPU.
 """
@@ -41,6 +42,21 @@ def build_runtime() -> str:
           os.path.join(PKG, "csrc", "tgrt.cpp"), "-o", tmp, "-Wl,-soname,libtgrt.so",
           "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-lhiprtc",
           "-Wl,-rpath," + os.path.join(ROCM, "lib")])
+    os.replace(tmp, out)
+    return out
+
+
+def build_vendor() -> Optional[str]:
+    """libtg_vendor.so (rocSPARSE comparison); skipped when rocSPARSE is absent."""
+    if not os.path.exists(os.path.join(ROCM, "include", "rocsparse", "rocsparse.h")):
+        return None
+    out = os.path.join(PKG, "_lib", "libtg_vendor.so")
+    tmp = out + ".tmp%d" % os.getpid()
+    cxx = os.environ.get("CXX") or shutil.which("g++") or "c++"
+    _run([cxx, "-std=c++17", "-O2", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__",
+          "-Wno-deprecated-declarations", "-I", os.path.join(ROCM, "include"),
+          os.path.join(PKG, "csrc", "vendor.cpp"), "-o", tmp, "-L", os.path.join(ROCM, "lib"),
+          "-lrocsparse", "-lamdhip64", "-Wl,-rpath," + os.path.join(ROCM, "lib")])
     os.replace(tmp, out)
     return out
 
@@ -84,6 +100,7 @@ def build_all(verbose: bool = True) -> None:
     path = build_runtime()
     if verbose:
         print("[build] runtime %s (%.1fs)" % (path, time.time() - t0))
+    build_vendor()
     build_oracle()
     if verbose:
         print("[build] oracle (%.1fs)" % (time.time() - t0))

@@ -1,0 +1,96 @@
+// libtg_vendor: rocSPARSE CSR SpMV timed on the same device buffers as the
+// generated kernels, for the vendor comparison the reference runs against
+// cuSPARSE (reference scripts/compare_cusparse.py:80-96).  Not on the product
+// path: nothing in tilegen_amd's launch/verify code calls it.
+//
+// One entry point, plain C types: it builds one rocSPARSE descriptor set per
+// argument set (rotation over input copies, as in tg_time_launches), runs the
+// preprocess stage once per set outside the timed region, then times `iters`
+// compute-stage calls with hipEvents recorded around each call on the
+// handle's stream.
+#include <hip/hip_runtime_api.h>
+#include <rocsparse/rocsparse.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <vector>
+
+namespace {
+thread_local char g_msg[512] = "";
+int fail(int code, const char* what) {
+  std::snprintf(g_msg, sizeof(g_msg), "%s failed (%d)", what, code);
+  return code ? code : -1;
+}
+}  // namespace
+
+extern "C" {
+
+const char* tgv_vendor_last_error(void) { return g_msg; }
+
+// sets: n_sets x 5 device pointers (indptr, indices, data, x, y).
+// alg: rocsparse_spmv_alg value (2 adaptive, 3 rowsplit, 7 lrb, 8 nnzsplit).
+int tgv_vendor_spmv_time(int alg, int64_t M, int64_t N, int64_t nnz, const uint64_t* sets,
+                         int n_sets, int warmup, int iters, float* ms_each, float* wall_ms) {
+  if (!sets || n_sets <= 0 || iters <= 0 || !ms_each) return fail(-1, "arguments");
+  rocsparse_handle h;
+  rocsparse_status st = rocsparse_create_handle(&h);
+  if (st != rocsparse_status_success) return fail(st, "rocsparse_create_handle");
+  hipStream_t stream;
+  hipStreamCreateWithFlags(&stream, hipStreamNonBlocking);
+  rocsparse_set_stream(h, stream);
+  const double alpha = 1.0, beta = 0.0;
+  std::vector<rocsparse_spmat_descr> A(n_sets);
+  std::vector<rocsparse_dnvec_descr> X(n_sets), Y(n_sets);
+  std::vector<void*> buf(n_sets, nullptr);
+  int rc = 0;
+  for (int s = 0; s < n_sets && rc == 0; ++s) {
+    const uint64_t* p = sets + 5 * s;
+    st = rocsparse_create_csr_descr(&A[s], M, N, nnz, (void*)p[0], (void*)p[1], (void*)p[2],
+                                    rocsparse_indextype_i64, rocsparse_indextype_i64,
+                                    rocsparse_index_base_zero, rocsparse_datatype_f64_r);
+    if (st == rocsparse_status_success)
+      st = rocsparse_create_dnvec_descr(&X[s], N, (void*)p[3], rocsparse_datatype_f64_r);
+    if (st == rocsparse_status_success)
+      st = rocsparse_create_dnvec_descr(&Y[s], M, (void*)p[4], rocsparse_datatype_f64_r);
+    size_t bytes = 0;
+    if (st == rocsparse_status_success)
+      st = rocsparse_spmv(h, rocsparse_operation_none, &alpha, A[s], X[s], &beta, Y[s],
+                          rocsparse_datatype_f64_r, (rocsparse_spmv_alg)alg,
+                          rocsparse_spmv_stage_buffer_size, &bytes, nullptr);
+    if (st == rocsparse_status_success && bytes) {
+      if (hipMalloc(&buf[s], bytes) != hipSuccess) st = rocsparse_status_memory_error;
+    }
+    if (st == rocsparse_status_success)
+      st = rocsparse_spmv(h, rocsparse_operation_none, &alpha, A[s], X[s], &beta, Y[s],
+                          rocsparse_datatype_f64_r, (rocsparse_spmv_alg)alg,
+                          rocsparse_spmv_stage_preprocess, &bytes, buf[s]);
+    if (st != rocsparse_status_success) rc = fail(st, "rocsparse setup");
+  }
+  std::vector<hipEvent_t> ev(2 * iters);
+  for (auto& e : ev) hipEventCreate(&e);
+  for (int i = 0; rc == 0 && i < warmup + iters; ++i) {
+    const int s = i % n_sets, t = i - warmup;
+    size_t bytes = 0;
+    if (t >= 0) hipEventRecord(ev[2 * t], stream);
+    st = rocsparse_spmv(h, rocsparse_operation_none, &alpha, A[s], X[s], &beta, Y[s],
+                        rocsparse_datatype_f64_r, (rocsparse_spmv_alg)alg,
+                        rocsparse_spmv_stage_compute, &bytes, buf[s]);
+    if (t >= 0) hipEventRecord(ev[2 * t + 1], stream);
+    if (st != rocsparse_status_success) rc = fail(st, "rocsparse_spmv compute");
+  }
+  hipStreamSynchronize(stream);
+  for (int t = 0; rc == 0 && t < iters; ++t) hipEventElapsedTime(&ms_each[t], ev[2 * t], ev[2 * t + 1]);
+  if (rc == 0 && wall_ms) hipEventElapsedTime(wall_ms, ev[0], ev[2 * iters - 1]);
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  for (int s = 0; s < n_sets; ++s) {
+    if (buf[s]) (void)hipFree(buf[s]);
+    if (A[s]) rocsparse_destroy_spmat_descr(A[s]);
+    if (X[s]) rocsparse_destroy_dnvec_descr(X[s]);
+    if (Y[s]) rocsparse_destroy_dnvec_descr(Y[s]);
+  }
+  rocsparse_destroy_handle(h);
+  (void)hipStreamDestroy(stream);
+  return rc;
+}
+
+}  // extern "C"

@@ -13,18 +13,21 @@ from typing import Dict, List
 from .codegen import Config
 
 TUNED: Dict[str, Config] = {
+    # winners of an exhaustive sweep of the legal CDNA4 space on one MI355X,
+    # cold (rotated) inputs, GPU-event kernel time
     # 16 nonzeros per row: 8 lanes x 2 consecutive nonzeros (one 128-bit load of
-    # indices and one of values per lane), 8 rows per wave, 4 rows per lane group
-    "c1": Config(tile_size=128, threads_per_row=8, unroll=2, vector_width=1, block_size=256),
+    # indices and one of values per lane), 8 rows per wave
+    "c1": Config(tile_size=16, threads_per_row=8, unroll=2, vector_width=1, block_size=128),
     # 7 nonzeros per row: 4 lanes x 2
-    "c2": Config(tile_size=256, threads_per_row=4, unroll=2, vector_width=1, block_size=256),
-    "c3a": Config(tile_size=64, threads_per_row=8, unroll=2, vector_width=1, block_size=256),
-    "c3b": Config(tile_size=32, threads_per_row=16, unroll=4, vector_width=1, block_size=256),
-    # K = 64: 32 lanes x 2 columns per row, 2 rows per wave, 4 nonzeros in flight
-    "c4": Config(tile_size=8, threads_per_row=32, unroll=4, vector_width=2, block_size=256),
-    # 16 nonzeros per row, K = 64: 4 lanes per nonzero x 2 columns per load
-    "c5": Config(tile_size=4, threads_per_row=4, unroll=2, vector_width=2, block_size=256),
-    "c5x25": Config(tile_size=4, threads_per_row=4, unroll=2, vector_width=2, block_size=256),
+    "c2": Config(tile_size=128, threads_per_row=4, unroll=2, vector_width=1, block_size=256),
+    # skewed rows: wide lane groups so the 5000-nonzero rows are not serial
+    "c3a": Config(tile_size=8, threads_per_row=32, unroll=4, vector_width=1, block_size=128),
+    "c3b": Config(tile_size=16, threads_per_row=64, unroll=4, vector_width=1, block_size=1024),
+    # K = 64: 16 lanes x 2 columns x 2 passes per row, 2 nonzeros' B rows in flight
+    "c4": Config(tile_size=16, threads_per_row=16, unroll=2, vector_width=2, block_size=64),
+    # 16 nonzeros per row, K = 64: 16 lanes per nonzero x 2 columns per load
+    "c5": Config(tile_size=16, threads_per_row=16, unroll=2, vector_width=2, block_size=256),
+    "c5x25": Config(tile_size=16, threads_per_row=16, unroll=2, vector_width=2, block_size=256),
 }
 
 # Swept by the GPU parity tests for every kernel: every threads_per_row the
