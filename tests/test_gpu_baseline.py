@@ -23,7 +23,7 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-10
 
 
-@pytest.mark.parametrize("case_id", ["c1", "c2", "c3a", "c3b", "c4", "c5"])
+@pytest.mark.parametrize("case_id", ["c1", "c2", "c3a", "c3b", "c4", "c5", "c5x25"])
 def test_baseline_case_parity(case_id, hip_ready):
     case = baseline_case(case_id)
     A = make_baseline(case_id)

@@ -15,6 +15,7 @@ import scipy.sparse as sp
 import oracle
 from tests.util import csr, mixed_257, ragged, rel_2, rel_inf
 from tilegen_amd.codegen import Config
+from tilegen_amd.matrices import make_baseline
 from tilegen_amd.schedules import TEST_KERNELS, TEST_SCHEDULES, schedule_id
 from tilegen_amd.variant import Variant
 from tilegen_amd.verify import _inputs_for, _reference, verify
@@ -139,3 +140,26 @@ def test_sddmm_empty_rows_and_long_rows(hip_ready):
     for cfg in (Config(tile_size=4, threads_per_row=4, unroll=2, vector_width=2, block_size=256),
                 Config(tile_size=1, threads_per_row=64, unroll=1, vector_width=1, block_size=64)):
         _check("sddmm", cfg, A, K=64)
+
+
+SKEW_CFGS = [
+    Config(tile_size=16, threads_per_row=8, unroll=2, block_size=128),
+    Config(tile_size=64, threads_per_row=1, unroll=1, block_size=64),     # long = 8 nonzeros
+    Config(tile_size=32, threads_per_row=4, unroll=3, block_size=256),
+    Config(tile_size=16, threads_per_row=64, unroll=4, block_size=1024),
+]
+
+
+@pytest.mark.parametrize("cfg", SKEW_CFGS, ids=[schedule_id(c) for c in SKEW_CFGS])
+@pytest.mark.parametrize("kernel", ["spmv", "fused_spmv_axpy"])
+def test_skewed_rows_workgroup_path(kernel, cfg, hip_ready):
+    """Rows longer than 8 lane-group steps go to the whole workgroup: one
+    enormous row, many long rows in one tile, long rows at the matrix end."""
+    cases = {
+        "power_law_small": make_baseline("c3a", scale=0.05),
+        "every_row_long": ragged(21, 200, 3000, 0, long_rows=[(r, 300 + r) for r in range(200)]),
+        "mixed": ragged(22, 3000, 8000, 6, empty_every=4,
+                        long_rows=[(0, 7000), (1, 9), (1500, 4000), (2998, 2500), (2999, 33)]),
+    }
+    for label, A in cases.items():
+        _check(kernel, cfg, A, K=1, label=label)

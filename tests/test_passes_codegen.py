@@ -158,7 +158,18 @@ def test_hip_markers():
 
 def test_hip_no_reduction_when_one_lane_per_row():
     src = _hip("spmv", Config(tile_size=128, threads_per_row=1, unroll=2, block_size=128))
-    assert "tg_segsum<" not in _code(src).split("tg_uniform(tg_i64 v)")[1]
+    body = _code(src).split("tg_uniform(tg_i64 v)")[1]
+    assert "acc[r] = tg_segsum" not in body
+    # only the workgroup path for long rows reduces across lanes
+    assert body.count("tg_segsum<") == 1 and "cacc = tg_segsum<64>(cacc);" in body
+
+
+def test_hip_long_rows_go_to_the_workgroup_only_when_tiled():
+    cfg = Config(tile_size=64, threads_per_row=4, unroll=2, block_size=256)
+    tiled = _hip("spmv", cfg)
+    assert "coop[r] = re[r] - rs[r] > 64;" in tiled  # 8 steps of 4 lanes x 2 nonzeros
+    assert "s_long[atomicAdd(&s_nlong, 1)] = lr;" in tiled
+    assert "s_long[" not in _hip("spmv", cfg, skip=("tiling",))
 
 
 def test_skipping_tiling_changes_hip_and_cpu_code():

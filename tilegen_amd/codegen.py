@@ -681,7 +681,14 @@ def _check_hip_schedule(plan: Plan, low: Lowering) -> None:
 
 def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeometry,
                        out_name: str) -> None:
-    """y[row] = final(sum over the row's nonzeros of value_expr)."""
+    """y[row] = final(sum over the row's nonzeros of value_expr).
+
+    Tiled variants also balance skewed rows without any preprocessing: a row
+    longer than LONG nonzeros (8 lane-group steps) is not walked by its lane
+    group; the group appends it to an LDS list, and after the lane-group phase
+    the whole workgroup takes each listed row in turn with coalesced loads and
+    a wave + LDS reduction.
+    """
     B, TPR = geo.block, max(1, low.threads_per_row)
     U = max(1, low.unroll)
     SLOTS = B // TPR
@@ -689,6 +696,9 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     R = (TR + SLOTS - 1) // SLOTS
     ALIGN = 2 if U % 2 == 0 else 1
     STEP = TPR * U
+    LONG = 8 * STEP
+    WAVES = B // WAVE
+    coop = low.tiled
     row = plan.row_idx.name
     col = plan.col_idx.name
 
@@ -699,6 +709,10 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     if low.tiled:
         w("// row pointers of this tile, staged once in LDS")
         w("__shared__ tg_i64 s_ptr[%d];" % (TR + 1))
+        w("__shared__ int s_long[%d];   // rows left to the whole workgroup" % TR)
+        w("__shared__ int s_nlong;")
+        w("__shared__ double s_red[%d];" % WAVES)
+        w("if (threadIdx.x == 0) s_nlong = 0;")
         w.open("for (int t = threadIdx.x; t <= %d; t += %d)" % (TR, B))
         w("const tg_i64 r = row0 + t;")
         w("s_ptr[t] = indptr[r < row_end ? r : row_end];")
@@ -706,6 +720,8 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("__syncthreads();")
     w("tg_i64 rs[%d], re[%d];" % (R, R))
     w("double acc[%d];" % R)
+    if coop:
+        w("bool coop[%d];" % R)
     w("#pragma unroll")
     w.open("for (int r = 0; r < %d; ++r)" % R)
     w("const int lr = slot + r * %d;" % SLOTS)
@@ -718,11 +734,19 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("const tg_i64 ri = live ? row0 + lr : 0;")
         w("rs[r] = live ? indptr[ri] : 0;")
         w("re[r] = live ? indptr[ri + 1] : 0;")
+    if coop:
+        w("coop[r] = re[r] - rs[r] > %d;" % LONG)
+        w.open("if (coop[r])")
+        w("if (lane == 0) s_long[atomicAdd(&s_nlong, 1)] = lr;")
+        w("re[r] = rs[r];  // the lane group skips it")
+        w.close()
     w("acc[r] = 0.0;")
     w.close()
 
-    def step(q: str, r: str) -> None:
-        """Load U consecutive nonzeros at q (masked to the row), gather, FMA."""
+    gathered = _gather_operand(plan)
+
+    def step(q: str, lo: str, hi: str, acc: str) -> None:
+        """Load U consecutive nonzeros at q (masked to [lo, hi)), gather, FMA."""
         w("tg_i64 ci[%d]; double cv[%d];" % (U, U))
         if U % 2 == 0:
             w.open("if (%s + %d <= nnz)" % (q, U))
@@ -745,15 +769,14 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("#pragma unroll")
         w.open("for (int u = 0; u < %d; ++u)" % U)
         w("const tg_i64 pu = %s + u;" % q)
-        w("const bool in_row = pu >= rs[%s] && pu < re[%s];" % (r, r))
+        w("const bool in_row = pu >= %s && pu < %s;" % (lo, hi))
         w("cv[u] = in_row ? cv[u] : 0.0;")
         w("ci[u] = in_row ? ci[u] : 0;")
-        w("xv[u] = %s;" % _cexpr(_gather_operand(plan), _Env({row: "row", col: "ci[u]"},
-                                                              p="pu")))
+        w("xv[u] = %s;" % _cexpr(gathered, _Env({row: "row", col: "ci[u]"}, p="pu")))
         w.close()
         w("#pragma unroll")
         w.open("for (int u = 0; u < %d; ++u)" % U)
-        w("acc[%s] += %s;" % (r, _value_with(plan, "cv[u]", "xv[u]", row, "ci[u]")))
+        w("%s += %s;" % (acc, _value_with(plan, "cv[u]", "xv[u]", row, "ci[u]")))
         w.close()
 
     w("// first step of every row in flight before any accumulation")
@@ -763,7 +786,7 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w("(void)row;")
     w("const tg_i64 q = (rs[r] & ~(tg_i64)%d) + (tg_i64)lane * %d;" % (ALIGN - 1, U))
     w.open("if (q < re[r] && rs[r] < re[r])")
-    step("q", "r")
+    step("q", "rs[r]", "re[r]", "acc[r]")
     w.close()
     w.close()
     w("// remaining steps (rows longer than %d nonzeros)" % (STEP - ALIGN + 1))
@@ -774,7 +797,7 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w("#pragma unroll 1")
     w.open("for (tg_i64 q = (rs[r] & ~(tg_i64)%d) + (tg_i64)lane * %d + %d; q < re[r]; q += %d)"
            % (ALIGN - 1, U, STEP, STEP))
-    step("q", "r")
+    step("q", "rs[r]", "re[r]", "acc[r]")
     w.close()
     w.close()
     w("#pragma unroll")
@@ -783,11 +806,41 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("acc[r] = tg_segsum<%d>(acc[r]);" % TPR)
     w("const int lr = slot + r * %d;" % SLOTS)
     w("const tg_i64 row = row0 + lr;")
-    w.open("if (%slr < %d && row < row_end)" % ("lane == 0 && " if TPR > 1 else "", TR))
+    w.open("if (%slr < %d && row < row_end%s)" % ("lane == 0 && " if TPR > 1 else "", TR,
+                                                   " && !coop[r]" if coop else ""))
     env = _Env({row: "row"}, acc="acc[r]")
     w("%s[%s] = %s;" % (out_name, _offset(plan.out_tensor, plan.out.indices, env),
                          _cexpr(plan.final_expr, env)))
     w.close()
+    w.close()
+    if not coop:
+        return
+    w("// long rows: the whole workgroup, one row at a time")
+    w("__syncthreads();")
+    w("const int n_long = s_nlong;")
+    w("#pragma unroll 1")
+    w.open("for (int k = 0; k < n_long; ++k)")
+    w("const int lr = s_long[k];")
+    w("const tg_i64 row = row0 + lr;")
+    w("const tg_i64 crs = s_ptr[lr], cre = s_ptr[lr + 1];")
+    w("double cacc = 0.0;")
+    w("#pragma unroll 1")
+    w.open("for (tg_i64 q = (crs & ~(tg_i64)%d) + (tg_i64)threadIdx.x * %d; q < cre; q += %d)"
+           % (ALIGN - 1, U, B * U))
+    step("q", "crs", "cre", "cacc")
+    w.close()
+    w("cacc = tg_segsum<64>(cacc);")
+    w("if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = cacc;")
+    w("__syncthreads();")
+    w.open("if (threadIdx.x == 0)")
+    w("double t = 0.0;")
+    w("#pragma unroll")
+    w("for (int v = 0; v < %d; ++v) t += s_red[v];" % WAVES)
+    env = _Env({row: "row"}, acc="t")
+    w("%s[%s] = %s;" % (out_name, _offset(plan.out_tensor, plan.out.indices, env),
+                         _cexpr(plan.final_expr, env)))
+    w.close()
+    w("__syncthreads();")
     w.close()
 
 

@@ -20,9 +20,10 @@ TUNED: Dict[str, Config] = {
     "c1": Config(tile_size=16, threads_per_row=8, unroll=2, vector_width=1, block_size=128),
     # 7 nonzeros per row: 4 lanes x 2
     "c2": Config(tile_size=128, threads_per_row=4, unroll=2, vector_width=1, block_size=256),
-    # skewed rows: wide lane groups so the 5000-nonzero rows are not serial
-    "c3a": Config(tile_size=8, threads_per_row=32, unroll=4, vector_width=1, block_size=128),
-    "c3b": Config(tile_size=16, threads_per_row=64, unroll=4, vector_width=1, block_size=1024),
+    # skewed rows: short rows on 8/32-lane groups, rows over 8 group steps
+    # (128 / 512 nonzeros) taken by the whole workgroup
+    "c3a": Config(tile_size=64, threads_per_row=8, unroll=2, vector_width=1, block_size=512),
+    "c3b": Config(tile_size=32, threads_per_row=32, unroll=2, vector_width=1, block_size=1024),
     # K = 64: 16 lanes x 2 columns x 2 passes per row, 2 nonzeros' B rows in flight
     "c4": Config(tile_size=16, threads_per_row=16, unroll=2, vector_width=2, block_size=64),
     # 16 nonzeros per row, K = 64: 16 lanes per nonzero x 2 columns per load
