@@ -2,7 +2,8 @@
 
 1. ``tilegen_amd/_lib/libtgrt.so`` (the runtime, include/tgrt.h) with the host
    C++ compiler against the ROCm HIP runtime and hipRTC;
-2. ``libtg_vendor.so``, the rocSPARSE comparison (when rocSPARSE is installed);
+2. ``libtg_vendor.so``, the rocSPARSE comparison (when rocSPARSE is installed),
+   and ``tilegen_bench``, the native host harness (TGM1 matrix + variant library);
 3. the test oracle (``oracle/Makefile``: the C restatement, and the
    reference's own ref.cpp where its sources are present);
 4. the hipRTC code objects and C launchers of every named schedule
@@ -61,6 +62,19 @@ def build_vendor() -> Optional[str]:
     return out
 
 
+def build_harness() -> str:
+    """tilegen_bench, the native host harness (csrc/bench_main.cpp)."""
+    lib_dir = os.path.join(PKG, "_lib")
+    out = os.path.join(lib_dir, "tilegen_bench")
+    tmp = out + ".tmp%d" % os.getpid()
+    cxx = os.environ.get("CXX") or shutil.which("g++") or "c++"
+    _run([cxx, "-std=c++17", "-O2", "-Wall", "-I", os.path.join(REPO, "include"),
+          os.path.join(PKG, "csrc", "bench_main.cpp"), "-o", tmp, "-L", lib_dir, "-ltgrt",
+          "-ldl", "-Wl,-rpath," + lib_dir])
+    os.replace(tmp, out)
+    return out
+
+
 def build_oracle() -> None:
     _run(["make", "-s", "-C", os.path.join(REPO, "oracle")])
 
@@ -101,6 +115,7 @@ def build_all(verbose: bool = True) -> None:
     if verbose:
         print("[build] runtime %s (%.1fs)" % (path, time.time() - t0))
     build_vendor()
+    build_harness()
     build_oracle()
     if verbose:
         print("[build] oracle (%.1fs)" % (time.time() - t0))

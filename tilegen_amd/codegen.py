@@ -994,6 +994,8 @@ def _hip_sparse_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeo
     w("const tg_i64 rs = tg_uniform(indptr[row]);")
     w("const tg_i64 re = tg_uniform(indptr[row + 1]);")
     w("const double* __restrict__ urow = %s + row * %s;" % (u_name, kext))
+    _hip_sparse_out_fast(w, plan, TPR, U, V, SLOTS, out_name, u_name, v_name, kext)
+    w.open("else")
     w("#pragma unroll 1")
     w.open("for (tg_i64 p0 = rs; p0 < re; p0 += %d)" % SLOTS)
     w("const tg_i64 p = p0 + slot;")
@@ -1055,6 +1057,76 @@ def _hip_sparse_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeo
     env = _Env({plan.row_idx.name: "row"}, p="p", acc="acc")
     w.open("if (valid%s)" % (" && kq == 0" if TPR > 1 else ""))
     w("%s[p] = %s;" % (out_name, _cexpr(plan.final_expr, env)))
+    w.close()
+    w.close()
+    w.close()  # else (general path)
+    w.close()
+
+
+def _hip_sparse_out_fast(w: _W, plan: Plan, TPR: int, U: int, V: int, SLOTS: int,
+                         out_name: str, u_name: str, v_name: str, kext: str) -> None:
+    """SDDMM path for K <= TPR*V*U: each lane keeps its slice of U[row, :] in
+    registers for the whole row, and every lane group has two nonzeros (index,
+    value and V-row slice) in flight before any FMA.  Opens an ``if``; the
+    caller emits the general path in the matching ``else``."""
+    W = V
+    KCAP = TPR * V * U
+    E = U * W
+    cond = "%s <= %d" % (kext, KCAP) + (" && vec_ok" if V == 2 else "")
+    w.open("if (%s)" % cond)
+    w("// the row's U slice stays in registers; two nonzeros per lane group in flight")
+    w("double ur[%d];" % E)
+    w("#pragma unroll")
+    w.open("for (int u = 0; u < %d; ++u)" % U)
+    w("const tg_i64 k = (tg_i64)kq * %d + u * %d;" % (W, TPR * W))
+    if W == 2:
+        w.open("if (k < %s)" % kext)
+        w("const tg_f64x2 t = *(const tg_f64x2*)(urow + k);")
+        w("ur[2 * u] = t.x; ur[2 * u + 1] = t.y;")
+        w.close()
+        w("else { ur[2 * u] = 0.0; ur[2 * u + 1] = 0.0; }")
+    else:
+        w("ur[u] = k < %s ? urow[k] : 0.0;" % kext)
+    w.close()
+    w("#pragma unroll 1")
+    w.open("for (tg_i64 p0 = rs; p0 < re; p0 += %d)" % (2 * SLOTS))
+    w("const tg_i64 pa = p0 + slot, pb = pa + %d;" % SLOTS)
+    w("const bool va = pa < re, vb = pb < re;")
+    w("const tg_i64 ja = va ? indices[pa] : 0, jb = vb ? indices[pb] : 0;")
+    w("const double da = va ? data[pa] : 0.0, db = vb ? data[pb] : 0.0;")
+    w("const double* __restrict__ vra = %s + ja * %s;" % (v_name, kext))
+    w("const double* __restrict__ vrb = %s + jb * %s;" % (v_name, kext))
+    w("double xa[%d], xb[%d];" % (E, E))
+    w("#pragma unroll")
+    w.open("for (int u = 0; u < %d; ++u)" % U)
+    w("const tg_i64 k = (tg_i64)kq * %d + u * %d;" % (W, TPR * W))
+    w("const bool in_k = k < %s;" % kext)
+    if W == 2:
+        w.open("if (va && in_k)")
+        w("const tg_f64x2 t = *(const tg_f64x2*)(vra + k);")
+        w("xa[2 * u] = t.x; xa[2 * u + 1] = t.y;")
+        w.close()
+        w("else { xa[2 * u] = 0.0; xa[2 * u + 1] = 0.0; }")
+        w.open("if (vb && in_k)")
+        w("const tg_f64x2 t = *(const tg_f64x2*)(vrb + k);")
+        w("xb[2 * u] = t.x; xb[2 * u + 1] = t.y;")
+        w.close()
+        w("else { xb[2 * u] = 0.0; xb[2 * u + 1] = 0.0; }")
+    else:
+        w("xa[u] = (va && in_k) ? vra[k] : 0.0;")
+        w("xb[u] = (vb && in_k) ? vrb[k] : 0.0;")
+    w.close()
+    w("double acca = 0.0, accb = 0.0;")
+    w("#pragma unroll")
+    w("for (int e = 0; e < %d; ++e) { acca += ur[e] * xa[e]; accb += ur[e] * xb[e]; }" % E)
+    if TPR > 1:
+        w("acca = tg_segsum<%d>(acca);" % TPR)
+        w("accb = tg_segsum<%d>(accb);" % TPR)
+    env_a = _Env({plan.row_idx.name: "row"}, p="pa", acc="acca", data="da")
+    env_b = _Env({plan.row_idx.name: "row"}, p="pb", acc="accb", data="db")
+    w.open("if (kq == 0)" if TPR > 1 else "")
+    w("if (va) %s[pa] = %s;" % (out_name, _cexpr(plan.final_expr, env_a)))
+    w("if (vb) %s[pb] = %s;" % (out_name, _cexpr(plan.final_expr, env_b)))
     w.close()
     w.close()
     w.close()
