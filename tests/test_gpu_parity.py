@@ -163,3 +163,26 @@ def test_skewed_rows_workgroup_path(kernel, cfg, hip_ready):
     }
     for label, A in cases.items():
         _check(kernel, cfg, A, K=1, label=label)
+
+
+CHUNK_CFGS = [
+    Config(tile_size=16, threads_per_row=16, unroll=2, vector_width=2, block_size=256),
+    Config(tile_size=8, threads_per_row=64, unroll=1, vector_width=1, block_size=128),
+    Config(tile_size=64, threads_per_row=4, unroll=8, vector_width=2, block_size=256),
+    Config(tile_size=32, threads_per_row=1, unroll=16, vector_width=2, block_size=64),
+]
+
+
+@pytest.mark.parametrize("cfg", CHUNK_CFGS, ids=[schedule_id(c) for c in CHUNK_CFGS])
+def test_sddmm_chunked_path(cfg, hip_ready):
+    """K covered by one lane group's registers: lane groups own adjacent rows,
+    chunks of TPR nonzeros with broadcast column indices.  Dense 4x4 blocks
+    (rows sharing columns), rows of different lengths in one wave, rows longer
+    than several chunks, empty rows, K below the register capacity."""
+    cases = {
+        "blocked": make_baseline("c5", scale=0.01),
+        "ragged": ragged(31, 700, 900, 37, empty_every=5, long_rows=[(3, 500), (4, 65)]),
+    }
+    for label, A in cases.items():
+        for K in (64, 40, 2):
+            _check("sddmm", cfg, A, K=K, label="%s K=%d" % (label, K))

@@ -238,9 +238,10 @@ def test_launch_geometry_covers_every_row():
     sd = _run(standard_kernels()["sddmm"], Config(tile_size=8, threads_per_row=4,
                                                    block_size=256), "hip")
     assert launch_geometry(_plan(sd), _lowering(sd)).rows_per_block == 8
+    # untiled SDDMM: one row per lane group, as for SpMV
     untiled = _run(standard_kernels()["sddmm"], Config(threads_per_row=4, block_size=256),
                    "hip", skip=("tiling",))
-    assert launch_geometry(_plan(untiled), _lowering(untiled)).rows_per_block == 4
+    assert launch_geometry(_plan(untiled), _lowering(untiled)).rows_per_block == 64
 
 
 @pytest.mark.parametrize("bad", [Config(block_size=96), Config(threads_per_row=3),

@@ -80,32 +80,45 @@ def build_oracle() -> None:
 
 
 def warm_cache(verbose: bool = False) -> int:
-    """Compile every named schedule for every kernel it applies to."""
+    """Compile every named schedule for every kernel it applies to, and the
+    one-pass-skipped variants the pass ablation times."""
     from . import runtime
     runtime._LIB = None  # pick up a freshly built library
+    from .ablation import DEFAULT_CASES
     from .codegen import Config, generate
     from .dsl import standard_kernels
     from .matrices import baseline_case
+    from .passes import PASS_NAMES
     from .schedules import TEST_KERNELS, TEST_SCHEDULES, TUNED
     from .verify import compile_generated
 
     kernels = standard_kernels()
     todo = []
     for case_id, cfg in TUNED.items():
-        todo.append((baseline_case(case_id).kernel, cfg))
+        todo.append((baseline_case(case_id).kernel, cfg, ()))
     for name in TEST_KERNELS:
         for cfg in TEST_SCHEDULES:
-            todo.append((name, cfg))
+            todo.append((name, cfg, ()))
         todo.append((name, Config(tile_size=32, threads_per_row=4, unroll=2, vector_width=1,
-                                  block_size=256, inject_bug=True)))
+                                  block_size=256, inject_bug=True), ()))
+    for name, cases in DEFAULT_CASES.items():
+        for case_id in cases:
+            todo += [(name, TUNED[case_id], skip) for skip in [()] + [(p,) for p in PASS_NAMES]]
     workdir = os.path.join(REPO, "build", "generated")
-    n = 0
-    for name, cfg in todo:
-        gen = generate(kernels[name], cfg, "hip", outdir=workdir)
+    n, seen = 0, set()
+    for name, cfg, skip in todo:
+        gen = generate(kernels[name], cfg, "hip", outdir=workdir, skip_passes=skip)
+        if gen.filename in seen:
+            continue
+        seen.add(gen.filename)
+        if skip:
+            full = generate(kernels[name], cfg, "hip", write=False)
+            if gen.abi_args != full.abi_args:
+                continue  # the ablation reports these as invalid and never runs them
         compile_generated(gen, "hip", workdir)
         n += 1
         if verbose:
-            print("[build] %s %s" % (name, cfg.short()))
+            print("[build] %s %s %s" % (name, cfg.short(), " ".join(skip)))
     return n
 
 

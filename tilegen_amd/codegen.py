@@ -27,9 +27,13 @@ backend "hip"
         (column, value) pairs arrive through the scalar unit.  C is written
         exactly once per element (no read-modify-write).
     sparse_out (sddmm)
-        one wave per row; ThreadsPerRow(k) lanes split the K-long dot product
-        of one nonzero (64/k nonzeros per wave at once), Vectorize(2) =
-        128-bit loads of U and V rows, Unroll(u) = u K-chunks in flight.
+        ThreadsPerRow(k) lanes split the K-long dot product of one nonzero,
+        Vectorize(2) = 128-bit loads of U and V rows, Unroll(u) = u K-chunks
+        per lane.  When k*V*u covers K: one lane group per row (64/k adjacent
+        rows per wave, so rows of a dense block gather the same V rows in one
+        instruction), U[row, :] held in registers, column indices loaded k at
+        a time and broadcast across the group, V gathers batched ahead of the
+        FMAs, one coalesced store per k outputs.  Otherwise one wave per row.
     elementwise (axpy)
         one lane per element.
 
@@ -634,6 +638,13 @@ __device__ __forceinline__ tg_i64 tg_uniform(tg_i64 v) {
   const int hi = __builtin_amdgcn_readfirstlane((int)(v >> 32));
   return ((tg_i64)hi << 32) | (tg_i64)(unsigned)lo;
 }
+
+// Value of v held by lane src of the wave (ds_bpermute; every lane active).
+__device__ __forceinline__ tg_i64 tg_lane_bcast(tg_i64 v, int src) {
+  const int lo = __shfl((int)v, src);
+  const int hi = __shfl((int)(v >> 32), src);
+  return ((tg_i64)hi << 32) | (tg_i64)(unsigned)lo;
+}
 """
 
 
@@ -655,10 +666,9 @@ def launch_geometry(plan: Plan, low: Lowering) -> LaunchGeometry:
     tpr = max(1, low.threads_per_row)
     if plan.kind == "elementwise":
         return LaunchGeometry(B, B, 0, plan.row_extent)
-    if plan.kind == "sparse_out":
-        rows = low.tile if low.tiled else max(1, B // WAVE)
-        return LaunchGeometry(rows, B, 0, plan.row_extent)
     slots = max(1, B // tpr)
+    if plan.kind == "sparse_out":
+        return LaunchGeometry(low.tile if low.tiled else slots, B, 0, plan.row_extent)
     rows = low.tile if low.tiled else slots
     lds = 8 * (rows + 1) if (plan.kind == "scalar_reduce" and low.tiled) else 0
     return LaunchGeometry(rows, B, lds, plan.row_extent)
@@ -969,7 +979,12 @@ def _hip_row_dense_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
 
 def _hip_sparse_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeometry,
                     out_name: str, u_name: str, v_name: str, kext: str) -> None:
-    """out[p] = data[p] * dot(U[row, :], V[col, :]) over the row's nonzeros."""
+    """out[p] = data[p] * dot(U[row, :], V[col, :]) over the row's nonzeros.
+
+    Two paths in one kernel, chosen by K at run time: the chunked path of
+    ``_hip_sparse_out_fast`` when one lane group covers K with registers
+    (K <= TPR*V*U), else one wave per row with the lane groups spread over the
+    row's nonzeros and each group looping over K."""
     B, TPR = geo.block, max(1, low.threads_per_row)
     U = max(1, low.unroll)
     V = 2 if low.vector_width >= 2 else 1
@@ -981,11 +996,13 @@ def _hip_sparse_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeo
     w("const tg_i64 row0 = (tg_i64)blockIdx.x * %d;" % TR)
     w("const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / %d);" % WAVE)
     w("const int wl = threadIdx.x %% %d;" % WAVE)
-    w("const int kq = wl %% %d;      // lane within one nonzero's group" % TPR)
-    w("const int slot = wl / %d;     // which nonzero of the pass" % TPR)
+    w("const int kq = wl %% %d;      // lane within the group" % TPR)
+    w("const int slot = wl / %d;     // lane group within the wave" % TPR)
     if V == 2:
         w("const bool vec_ok = ((%s & 1) == 0) && ((((unsigned long long)%s) | "
           "((unsigned long long)%s)) & 15) == 0;" % (kext, u_name, v_name))
+    _hip_sparse_out_fast(w, plan, TPR, U, V, SLOTS, WAVES, TR, out_name, u_name, v_name, kext)
+    w.open("else")
     w("#pragma unroll 1")
     w.open("for (int r = 0; r < %d; ++r)" % R)
     w("const int lr = wave + r * %d;" % WAVES)
@@ -994,8 +1011,6 @@ def _hip_sparse_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeo
     w("const tg_i64 rs = tg_uniform(indptr[row]);")
     w("const tg_i64 re = tg_uniform(indptr[row + 1]);")
     w("const double* __restrict__ urow = %s + row * %s;" % (u_name, kext))
-    _hip_sparse_out_fast(w, plan, TPR, U, V, SLOTS, out_name, u_name, v_name, kext)
-    w.open("else")
     w("#pragma unroll 1")
     w.open("for (tg_i64 p0 = rs; p0 < re; p0 += %d)" % SLOTS)
     w("const tg_i64 p = p0 + slot;")
@@ -1059,77 +1074,106 @@ def _hip_sparse_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeo
     w("%s[p] = %s;" % (out_name, _cexpr(plan.final_expr, env)))
     w.close()
     w.close()
+    w.close()  # for r
     w.close()  # else (general path)
-    w.close()
 
 
-def _hip_sparse_out_fast(w: _W, plan: Plan, TPR: int, U: int, V: int, SLOTS: int,
-                         out_name: str, u_name: str, v_name: str, kext: str) -> None:
-    """SDDMM path for K <= TPR*V*U: each lane keeps its slice of U[row, :] in
-    registers for the whole row, and every lane group has two nonzeros (index,
-    value and V-row slice) in flight before any FMA.  Opens an ``if``; the
-    caller emits the general path in the matching ``else``."""
+def _sddmm_batch(TPR: int, E: int) -> int:
+    """V-row slices gathered per batch on the chunked SDDMM path: a power of
+    two, at most the chunk (TPR nonzeros) and at most 32 doubles of staging
+    per lane."""
+    nb = 1
+    while nb * 2 <= TPR and nb * 2 * E <= 32:
+        nb *= 2
+    return nb
+
+
+def _hip_sparse_out_fast(w: _W, plan: Plan, TPR: int, U: int, V: int, SLOTS: int, WAVES: int,
+                         TR: int, out_name: str, u_name: str, v_name: str, kext: str) -> None:
+    """SDDMM path for K <= TPR*V*U.  One lane group per row, SLOTS rows per
+    wave, consecutive rows side by side, so rows that share columns (dense
+    blocks) gather the same V rows in the same instruction.  Each lane keeps
+    its slice of U[row, :] in registers.  The row is walked in chunks of TPR
+    nonzeros: lane kq loads index and value of nonzero q+kq (one coalesced
+    load each), the column indices are broadcast across the group with lane
+    shuffles, the V-row slices of a batch are all in flight before any FMA,
+    lane kq keeps the dot product of nonzero q+kq, and the chunk ends with one
+    coalesced store.  Opens an ``if``; the caller emits the general path in
+    the matching ``else``."""
     W = V
     KCAP = TPR * V * U
     E = U * W
+    NB = _sddmm_batch(TPR, E)
     cond = "%s <= %d" % (kext, KCAP) + (" && vec_ok" if V == 2 else "")
     w.open("if (%s)" % cond)
-    w("// the row's U slice stays in registers; two nonzeros per lane group in flight")
+    w("// one lane group per row; chunks of %d nonzeros, V slices gathered %d at a time"
+      % (TPR, NB))
+    w("#pragma unroll 1")
+    w.open("for (int c = wave; c * %d < %d; c += %d)" % (SLOTS, TR, WAVES))
+    w("const int lr = c * %d + slot;" % SLOTS)
+    w("const tg_i64 row = row0 + lr;")
+    w("const bool live = lr < %d && row < row_end;" % TR)
+    w("const tg_i64 rs = live ? indptr[row] : 0;")
+    w("const tg_i64 len = live ? indptr[row + 1] - rs : 0;")
+    w("const double* __restrict__ urow = %s + (live ? row : 0) * %s;" % (u_name, kext))
     w("double ur[%d];" % E)
     w("#pragma unroll")
     w.open("for (int u = 0; u < %d; ++u)" % U)
     w("const tg_i64 k = (tg_i64)kq * %d + u * %d;" % (W, TPR * W))
     if W == 2:
-        w.open("if (k < %s)" % kext)
+        w.open("if (live && k < %s)" % kext)
         w("const tg_f64x2 t = *(const tg_f64x2*)(urow + k);")
         w("ur[2 * u] = t.x; ur[2 * u + 1] = t.y;")
         w.close()
         w("else { ur[2 * u] = 0.0; ur[2 * u + 1] = 0.0; }")
     else:
-        w("ur[u] = k < %s ? urow[k] : 0.0;" % kext)
+        w("ur[u] = (live && k < %s) ? urow[k] : 0.0;" % kext)
     w.close()
     w("#pragma unroll 1")
-    w.open("for (tg_i64 p0 = rs; p0 < re; p0 += %d)" % (2 * SLOTS))
-    w("const tg_i64 pa = p0 + slot, pb = pa + %d;" % SLOTS)
-    w("const bool va = pa < re, vb = pb < re;")
-    w("const tg_i64 ja = va ? indices[pa] : 0, jb = vb ? indices[pb] : 0;")
-    w("const double da = va ? data[pa] : 0.0, db = vb ? data[pb] : 0.0;")
-    w("const double* __restrict__ vra = %s + ja * %s;" % (v_name, kext))
-    w("const double* __restrict__ vrb = %s + jb * %s;" % (v_name, kext))
-    w("double xa[%d], xb[%d];" % (E, E))
+    w.open("for (tg_i64 q = 0; __builtin_amdgcn_ballot_w64(q < len) != 0; q += %d)" % TPR)
+    w("const bool mine = q + kq < len;")
+    w("const tg_i64 jl = mine ? indices[rs + q + kq] : 0;")
+    w("const double dl = mine ? data[rs + q + kq] : 0.0;")
+    w("double res = 0.0;")
+    w("#pragma unroll")
+    w.open("for (int n0 = 0; n0 < %d; n0 += %d)" % (TPR, NB))
+    w("double x[%d][%d];" % (NB, E))
+    w("#pragma unroll")
+    w.open("for (int n = 0; n < %d; ++n)" % NB)
+    if TPR > 1:
+        w("const tg_i64 j = tg_lane_bcast(jl, slot * %d + n0 + n);" % TPR)
+    else:
+        w("const tg_i64 j = jl;")
+    w("const bool v = q + n0 + n < len;")
+    w("const double* __restrict__ vr = %s + j * %s;" % (v_name, kext))
     w("#pragma unroll")
     w.open("for (int u = 0; u < %d; ++u)" % U)
     w("const tg_i64 k = (tg_i64)kq * %d + u * %d;" % (W, TPR * W))
-    w("const bool in_k = k < %s;" % kext)
     if W == 2:
-        w.open("if (va && in_k)")
-        w("const tg_f64x2 t = *(const tg_f64x2*)(vra + k);")
-        w("xa[2 * u] = t.x; xa[2 * u + 1] = t.y;")
+        w.open("if (v && k < %s)" % kext)
+        w("const tg_f64x2 t = *(const tg_f64x2*)(vr + k);")
+        w("x[n][2 * u] = t.x; x[n][2 * u + 1] = t.y;")
         w.close()
-        w("else { xa[2 * u] = 0.0; xa[2 * u + 1] = 0.0; }")
-        w.open("if (vb && in_k)")
-        w("const tg_f64x2 t = *(const tg_f64x2*)(vrb + k);")
-        w("xb[2 * u] = t.x; xb[2 * u + 1] = t.y;")
-        w.close()
-        w("else { xb[2 * u] = 0.0; xb[2 * u + 1] = 0.0; }")
+        w("else { x[n][2 * u] = 0.0; x[n][2 * u + 1] = 0.0; }")
     else:
-        w("xa[u] = (va && in_k) ? vra[k] : 0.0;")
-        w("xb[u] = (vb && in_k) ? vrb[k] : 0.0;")
+        w("x[n][u] = (v && k < %s) ? vr[k] : 0.0;" % kext)
     w.close()
-    w("double acca = 0.0, accb = 0.0;")
+    w.close()
     w("#pragma unroll")
-    w("for (int e = 0; e < %d; ++e) { acca += ur[e] * xa[e]; accb += ur[e] * xb[e]; }" % E)
+    w.open("for (int n = 0; n < %d; ++n)" % NB)
+    w("double acc = 0.0;")
+    w("#pragma unroll")
+    w("for (int e = 0; e < %d; ++e) acc += ur[e] * x[n][e];" % E)
     if TPR > 1:
-        w("acca = tg_segsum<%d>(acca);" % TPR)
-        w("accb = tg_segsum<%d>(accb);" % TPR)
-    env_a = _Env({plan.row_idx.name: "row"}, p="pa", acc="acca", data="da")
-    env_b = _Env({plan.row_idx.name: "row"}, p="pb", acc="accb", data="db")
-    w.open("if (kq == 0)" if TPR > 1 else "")
-    w("if (va) %s[pa] = %s;" % (out_name, _cexpr(plan.final_expr, env_a)))
-    w("if (vb) %s[pb] = %s;" % (out_name, _cexpr(plan.final_expr, env_b)))
+        w("acc = tg_segsum<%d>(acc);" % TPR)
+    w("if (kq == n0 + n) res = acc;")
     w.close()
     w.close()
-    w.close()
+    env = _Env({plan.row_idx.name: "row"}, p="(rs + q + kq)", acc="res", data="dl")
+    w("if (mine) %s[rs + q + kq] = %s;" % (out_name, _cexpr(plan.final_expr, env)))
+    w.close()  # for q
+    w.close()  # for c
+    w.close()  # if fast
 
 
 def _hip_elementwise(w: _W, plan: Plan, bound: str, geo: LaunchGeometry, out_name: str) -> None:
