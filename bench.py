@@ -18,6 +18,10 @@ roofline     per-kernel duration from start/stop events attached to each
 cpu_baseline the reference's own sequential cpp/src/ref.cpp (oracle/_ref, kind
              "reference"; else this repository's C restatement, kind "port"),
              one host core, on the full case matrix for a bounded number of calls
+cpu_openmp   this build's OpenMP CPU backend (the reference's ``_cpu_emit``
+             design) at the reference default schedule T32/TPR1/U1/V1/B128,
+             compiled on this host with g++ -O3 -march=native -fopenmp and run
+             on every OpenMP thread, host perf_counter around each call
 
 Cases are BASELINE.json's configs (tilegen_amd.matrices.baseline_ids()); the
 default c1 is the config the headline metric is quoted on.
@@ -126,6 +130,40 @@ def _cpu_baseline(kernel, A, ops, budget_s: float):
             oracle.compute(kernel, A, ops)
         sec = (time.perf_counter() - t0) / iters
     return kind, sec, iters
+
+
+def _omp_threads() -> int:
+    import ctypes
+    try:
+        return int(ctypes.CDLL("libgomp.so.1").omp_get_max_threads())
+    except OSError:
+        return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+
+
+def _openmp_baseline(kernel, A, ops, K, ref, nbytes, nflop, budget_s: float):
+    """Time the OpenMP variant of the reference default schedule on the host."""
+    from tilegen_amd.autotune import BASELINE, _make_caller, _time_host
+    from tilegen_amd.codegen import generate
+    from tilegen_amd.dsl import standard_kernels
+    from tilegen_amd.verify import compile_generated
+    workdir = os.path.join(ROOT, "build", "bench_cpu")
+    gen = generate(standard_kernels()[kernel], BASELINE, "cpu", outdir=workdir)
+    so, log = compile_generated(gen, "cpu", workdir)
+    data = (ops.get("x"), None, ops.get("B"), ops.get("U"), ops.get("V"), 1.0, 0.0)
+    caller, _out, _keep = _make_caller(so, kernel, A, data, K, "cpu")
+    t0 = time.perf_counter()
+    got = np.asarray(caller(), dtype=np.float64).reshape(np.shape(ref))
+    t1 = time.perf_counter() - t0
+    err = float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-300))
+    iters = int(max(5, min(2000, budget_s / max(t1, 1e-6))))
+    ms = _time_host(caller.launch, 2, iters)
+    med = float(np.median(ms)) * 1e-3
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": _omp_threads(),
+            "kind": "openmp backend", "schedule": BASELINE.short(),
+            "sample": "%d calls of the full matrix, median %.3f ms per call" % (iters, med * 1e3),
+            "gflops": round(nflop / med / 1e9, 3), "ms_median": round(med * 1e3, 4),
+            "ms_min": round(float(np.min(ms)), 4), "rel_err": err,
+            "compile": log.split(" with: ")[-1]}
 
 
 def main(argv=None) -> int:
@@ -257,6 +295,11 @@ def main(argv=None) -> int:
                "gflops": round(nflop / sec / 1e9, 3), "ms_per_call": round(sec * 1e3, 4)}
         _log("cpu baseline (%s): %.3f ms per call" % (kind, sec * 1e3))
 
+    omp = None
+    if not args.no_cpu:
+        omp = _openmp_baseline(case.kernel, A, ops, K, ref, nbytes, nflop, args.cpu_seconds / 2)
+        _log("cpu OpenMP backend (%d threads): %s" % (omp["cores"], omp["sample"]))
+
     for bufs in keep:
         for b in bufs.values():
             b.free()
@@ -297,6 +340,7 @@ def main(argv=None) -> int:
             "traffic": _traffic(case.kernel, args.case),
         },
         "cpu_baseline": cpu,
+        "cpu_openmp": omp,
         "vendor": vendor,
         "check_rel_err": err,
         "device": "%s %s" % (dev["name"], dev["arch"]),

@@ -112,9 +112,23 @@ def test_illegal_configs_pruned_with_reasons():
     assert set(SEARCH_SPACE["block_size"]) <= {64, 128, 256, 512, 1024}
 
 
-def test_sddmm_space_is_wave_per_row():
+def test_sddmm_space_follows_the_row_mapping():
+    """Chunked path (one group's registers cover K): tiles are multiples of the
+    lane groups per block; otherwise one wave per row: multiples of the waves."""
+    from tilegen_amd.autotune import sddmm_group_per_row
     cs = legal_configs("sddmm", 64)
-    assert cs and all(c.tile_size % (c.block_size // 64) == 0 for c in cs)
+    assert cs
+    for c in cs:
+        per = c.block_size // (c.threads_per_row if sddmm_group_per_row(c, 64) else 64)
+        assert c.tile_size % per == 0 and per <= c.tile_size <= 8 * per
+    assert any(sddmm_group_per_row(c, 64) for c in cs)
+    assert any(not sddmm_group_per_row(c, 64) for c in cs)
+    tuned = Config(tile_size=16, threads_per_row=16, unroll=2, vector_width=2, block_size=256)
+    assert sddmm_group_per_row(tuned, 64) and illegal_reason_for("sddmm", tuned, 64) is None
+    assert not sddmm_group_per_row(tuned, 65)  # odd K: no 128-bit path, wave per row
+    assert illegal_reason_for("sddmm", tuned, 130) is None  # wave per row: 4 rows per wave
+    small = Config(tile_size=4, threads_per_row=16, unroll=2, vector_width=2, block_size=256)
+    assert "lane group" in illegal_reason_for("sddmm", small, 64)  # 16 groups, 4 rows
 
 
 def test_tune_smoke_cpu(tmp_path):

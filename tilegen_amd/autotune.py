@@ -63,9 +63,9 @@ _LDS_LIMIT = 64 * 1024
 ROTATE_BYTES = 640 << 20
 
 
-def illegal_reason(cfg: Config) -> Optional[str]:
-    """Why a schedule is illegal on CDNA4, or None."""
-    B, tpr, T = cfg.block_size, cfg.threads_per_row, cfg.tile_size
+def _shape_reason(cfg: Config) -> Optional[str]:
+    """Block, lane-group and vector checks shared by every kernel."""
+    B, tpr = cfg.block_size, cfg.threads_per_row
     if B % _WAVE:
         return "block_size (%d) is not a multiple of the 64-lane wave" % B
     if B > 1024:
@@ -78,6 +78,15 @@ def illegal_reason(cfg: Config) -> Optional[str]:
         return "vector_width %d not supported (128-bit loads hold 2 x f64)" % cfg.vector_width
     if cfg.vector_width > cfg.unroll:
         return "vector_width (%d) > unroll (%d)" % (cfg.vector_width, cfg.unroll)
+    return None
+
+
+def illegal_reason(cfg: Config) -> Optional[str]:
+    """Why a schedule is illegal on CDNA4, or None."""
+    r = _shape_reason(cfg)
+    if r is not None:
+        return r
+    B, tpr, T = cfg.block_size, cfg.threads_per_row, cfg.tile_size
     slots = B // tpr
     if T < slots:
         return "tile_size (%d) < lane groups per block (%d): idle lanes" % (T, slots)
@@ -88,8 +97,31 @@ def illegal_reason(cfg: Config) -> Optional[str]:
     return None
 
 
+def sddmm_group_per_row(cfg: Config, K: int) -> bool:
+    """Whether the SDDMM variant takes its chunked path at this K (one lane
+    group per row, K covered by one group's registers) rather than one wave
+    per row."""
+    tpr, V = cfg.threads_per_row, 2 if cfg.vector_width >= 2 else 1
+    return K <= tpr * V * max(1, cfg.unroll) and (V == 1 or K % 2 == 0)
+
+
 def illegal_reason_for(kernel: str, cfg: Config, K: int = 8) -> Optional[str]:
     """Kernel-specific pruning on top of ``illegal_reason``."""
+    if kernel == "sddmm":
+        r = _shape_reason(cfg)
+        if r is not None:
+            return r
+        if cfg.threads_per_row * cfg.vector_width > max(K, 1):
+            return "threads_per_row x vector_width (%d) > K (%d)" % (
+                cfg.threads_per_row * cfg.vector_width, K)
+        if sddmm_group_per_row(cfg, K):
+            per, what = cfg.block_size // cfg.threads_per_row, "lane group"
+        else:
+            per, what = cfg.block_size // _WAVE, "wave"
+        if cfg.tile_size < per or cfg.tile_size > 8 * per:
+            return ("sddmm runs one row per %s at K=%d: tile_size must be 1..8 x %d"
+                    % (what, K, per))
+        return None
     r = illegal_reason(cfg)
     if r is not None:
         return r
@@ -98,24 +130,21 @@ def illegal_reason_for(kernel: str, cfg: Config, K: int = 8) -> Optional[str]:
     if kernel == "spmm" and cfg.threads_per_row * cfg.vector_width > max(_WAVE, 2 * K):
         return "threads_per_row x vector_width (%d) far exceeds K (%d)" % (
             cfg.threads_per_row * cfg.vector_width, K)
-    if kernel == "sddmm":
-        waves = cfg.block_size // _WAVE
-        if cfg.tile_size < waves or cfg.tile_size > 8 * waves:
-            return "sddmm runs one wave per row: tile_size must be 1..8 x waves per block"
-        if cfg.threads_per_row * cfg.vector_width > max(K, 1):
-            return "threads_per_row x vector_width (%d) > K (%d)" % (
-                cfg.threads_per_row * cfg.vector_width, K)
     return None
 
 
-def _sddmm_space() -> List[Config]:
+def _sddmm_space(K: int) -> List[Config]:
+    """Tiles of 1, 2 and 4 rows per lane group (chunked path) or per wave
+    (general path), whichever the variant takes at this K."""
     out = []
     for B, tpr, U, V in itertools.product([64, 128, 256, 512], [1, 2, 4, 8, 16, 32, 64],
                                           [1, 2, 4, 8], [1, 2]):
-        waves = B // _WAVE
+        probe = Config(threads_per_row=tpr, unroll=U, vector_width=V, block_size=B)
+        per = B // tpr if sddmm_group_per_row(probe, K) else B // _WAVE
         for mult in (1, 2, 4):
-            out.append(Config(tile_size=waves * mult, threads_per_row=tpr, unroll=U,
-                              vector_width=V, block_size=B))
+            if per * mult <= 4096:
+                out.append(Config(tile_size=per * mult, threads_per_row=tpr, unroll=U,
+                                  vector_width=V, block_size=B))
     return out
 
 
@@ -123,7 +152,7 @@ def enumerate_configs(kernel: Optional[str] = None, K: int = 8
                       ) -> List[Tuple[Config, Optional[str]]]:
     """Every raw schedule with its prune reason (None = legal)."""
     if kernel == "sddmm":
-        return [(c, illegal_reason_for(kernel, c, K)) for c in _sddmm_space()]
+        return [(c, illegal_reason_for(kernel, c, K)) for c in _sddmm_space(K)]
     keys = list(SEARCH_SPACE)
     out = []
     for combo in itertools.product(*(SEARCH_SPACE[k] for k in keys)):

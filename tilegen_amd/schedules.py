@@ -26,9 +26,11 @@ TUNED: Dict[str, Config] = {
     "c3b": Config(tile_size=32, threads_per_row=32, unroll=2, vector_width=1, block_size=1024),
     # K = 64: 16 lanes x 2 columns x 2 passes per row, 2 nonzeros' B rows in flight
     "c4": Config(tile_size=16, threads_per_row=16, unroll=2, vector_width=2, block_size=64),
-    # 16 nonzeros per row, K = 64: 16 lanes per nonzero x 2 columns per load
-    "c5": Config(tile_size=16, threads_per_row=16, unroll=2, vector_width=2, block_size=256),
-    "c5x25": Config(tile_size=16, threads_per_row=16, unroll=2, vector_width=2, block_size=256),
+    # K = 64 on the chunked SDDMM path: 8 lanes per row x 2 columns per load x 4
+    # loads cover K; 8 adjacent rows per wave (two 4x4 block rows), chunks of 8
+    # nonzeros, 4 V-row slices in flight per lane
+    "c5": Config(tile_size=16, threads_per_row=8, unroll=4, vector_width=2, block_size=128),
+    "c5x25": Config(tile_size=16, threads_per_row=8, unroll=4, vector_width=2, block_size=128),
 }
 
 # Swept by the GPU parity tests for every kernel: every threads_per_row the
