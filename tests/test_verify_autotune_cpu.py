@@ -156,3 +156,18 @@ def test_write_outputs_schema(tmp_path):
     assert 0 < len(data["top5"]["tiny"]) <= 5
     raw = json.load(open(str(full / "autotune.json")))
     assert raw["results"][0]["records"]
+
+
+def test_bench_openmp_leg_on_cpu():
+    """bench.py's cpu_openmp leg: the OpenMP backend at the reference default
+    schedule, checked against the float64 result it is given."""
+    import bench
+    from tilegen_amd.autotune import BASELINE
+    from tests.util import ragged
+    A = ragged(11, 300, 200, 12, empty_every=7)
+    x = np.random.default_rng(0).uniform(-1, 1, A.shape[1])
+    ref = A @ x
+    r = bench._openmp_baseline("spmv", A, {"x": x}, 1, ref, 1000, 100, 0.05)
+    assert r["kind"] == "openmp backend" and r["schedule"] == BASELINE.short()
+    assert r["rel_err"] <= 1e-12 and r["cores"] >= 1 and r["value"] > 0
+    assert "-fopenmp" in r["compile"]
