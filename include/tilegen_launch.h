@@ -3,8 +3,9 @@
  * library exports (one shared object per (kernel, schedule), produced by
  * tilegen_amd.verify.compile_generated).
  *
- * The three launch_* entry points are the reference's plugin interface for the
- * CSR hot path, with identical argument order and types: each reference
+ * The launch_* entry points are the reference's plugin interface for the CSR
+ * hot path (spmv, spmm, sddmm) and for the two standard kernels around it
+ * (fused_spmv_axpy, axpy), with identical argument order and types: each reference
  * variant is one `extern "C" void launch_<name>(...)` (reference
  * tilegen/codegen.py:226-280 `_abi`, :814-818; ctypes argtypes at
  * tilegen/verify.py:166-173 `_SIGNATURES`; dlsym binding at
@@ -46,6 +47,16 @@ void launch_spmm(const int64_t* indptr, const int64_t* indices, const double* da
 void launch_sddmm(const int64_t* indptr, const int64_t* indices, const double* data,
                   const double* U, const double* V, double* C, int64_t M, int64_t N,
                   int64_t K, int64_t nnz);
+
+/* z[i] = alpha * sum_p data[p] * x[indices[p]] + beta * w[i]  (reference
+ * dsl.py fused_spmv_axpy after loop_fusion; argtypes verify.py:170-171) */
+void launch_fused_spmv_axpy(const int64_t* indptr, const int64_t* indices, const double* data,
+                            const double* x, const double* w, double* z, double alpha,
+                            double beta, int64_t M, int64_t N, int64_t nnz);
+
+/* z[i] = alpha * x[i] + beta * w[i]  (reference dsl.py axpy; argtypes verify.py:172) */
+void launch_axpy(const double* x, const double* w, double* z, double alpha, double beta,
+                 int64_t M);
 
 /* Harness side of a variant library (no counterpart in the reference). */
 void* tgv_function(void);                  /* the variant's kernel, current device */

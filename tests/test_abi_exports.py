@@ -43,7 +43,7 @@ def test_runtime_exports_every_declared_symbol():
         assert hasattr(L, s)
 
 
-@pytest.mark.parametrize("kernel", ["spmv", "spmm", "sddmm"])
+@pytest.mark.parametrize("kernel", ["spmv", "spmm", "sddmm", "fused_spmv_axpy", "axpy"])
 def test_variant_library_exports_launch_abi(kernel, tmp_path):
     gen = generate(standard_kernels()[kernel], Config(tile_size=64, threads_per_row=8,
                                                       unroll=2, block_size=256),
@@ -61,7 +61,20 @@ def test_variant_library_exports_launch_abi(kernel, tmp_path):
     lib.tgv_geometry.argtypes = [ctypes.c_int64] * 4 + [ctypes.c_void_p] * 3
     assert lib.tgv_geometry(1000, 1000, 64, 5000, ctypes.byref(g), ctypes.byref(b),
                             ctypes.byref(l)) == 0
-    assert b.value == 256 and g.value * 64 >= 1000 if kernel != "sddmm" else g.value > 0
+    assert b.value == 256 and g.value * gen.geometry.rows_per_block >= 1000
+
+
+def test_header_signatures_match_generated_launchers():
+    """Each launch_* declaration in the header is the generated launcher's
+    signature, token for token."""
+    text = open(os.path.join(ROOT, "include", "tilegen_launch.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {m.group(1): " ".join(m.group(0).split())
+             for m in re.finditer(r"void (launch_[a-z_]+)\([^)]*\)", text)}
+    assert sorted(decls) == sorted("launch_%s" % k for k in standard_kernels())
+    for name in standard_kernels():
+        gen = generate(standard_kernels()[name], Config(), "hip", write=False)
+        assert " ".join(gen.abi_signature.split()) == decls["launch_%s" % name], name
 
 
 def test_runtime_error_reporting_without_device():
