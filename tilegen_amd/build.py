@@ -75,8 +75,8 @@ def build_harness() -> str:
     return out
 
 
-def build_oracle() -> None:
-    _run(["make", "-s", "-C", os.path.join(REPO, "oracle")])
+def build_oracle(force: bool = False) -> None:
+    _run(["make", "-s"] + (["-B"] if force else []) + ["-C", os.path.join(REPO, "oracle")])
 
 
 def warm_cache(verbose: bool = False) -> int:
@@ -122,14 +122,19 @@ def warm_cache(verbose: bool = False) -> int:
     return n
 
 
-def build_all(verbose: bool = True) -> None:
+def build_all(verbose: bool = True, force: bool = False) -> None:
+    """Build everything; ``force`` also recompiles the oracle and every cached
+    kernel variant instead of reusing up-to-date outputs."""
     t0 = time.time()
     path = build_runtime()
     if verbose:
         print("[build] runtime %s (%.1fs)" % (path, time.time() - t0))
     build_vendor()
     build_harness()
-    build_oracle()
+    build_oracle(force)
+    if force:
+        from .verify import cache_dir
+        shutil.rmtree(cache_dir(), ignore_errors=True)
     if verbose:
         print("[build] oracle (%.1fs)" % (time.time() - t0))
     n = warm_cache()
@@ -138,5 +143,5 @@ def build_all(verbose: bool = True) -> None:
 
 
 if __name__ == "__main__":
-    build_all(verbose=True)
+    build_all(verbose=True, force="--force" in sys.argv[1:])
     sys.exit(0)

@@ -14,7 +14,8 @@ committed commands (see ``commands()``):
 without the profiler, whose event-timed kernel average the trace is compared
 with.
 
-``python -m tilegen_amd.profiling --case c1 --root gpurun_out/prof`` writes
+``python -m tilegen_amd.profiling --case c1 --root <dir>`` (the ``-d`` directory the
+rocprofv3 commands wrote under) writes
 ``profiles/<kernel>_<case>.md`` (human summary with the exact commands) and
 ``profiles/<kernel>_<case>_pmc.json`` (the measured HBM bytes per launch that
 ``bench.py`` reports as ``roofline.traffic``).
@@ -38,7 +39,7 @@ BENCH_PMC = "python3 bench.py --case {case} --no-cpu --steps 20 --warmup 2"
 BENCH_TRACE = "python3 bench.py --case {case} --no-cpu"
 
 
-def commands(case: str, root: str = "gpurun_out/prof") -> Dict[str, str]:
+def commands(case: str, root: str = "rocprof_out") -> Dict[str, str]:
     """The rocprofv3 command lines whose outputs ``summarize`` reads."""
     d = os.path.join(root, case)
     return {
@@ -187,7 +188,7 @@ def summarize(case: str, root: str, out_dir: str, bench_json: Optional[str] = No
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="Summarize rocprofv3 CSV output into profiles/.")
     ap.add_argument("--case", required=True)
-    ap.add_argument("--root", default="gpurun_out/prof")
+    ap.add_argument("--root", default="rocprof_out")
     ap.add_argument("--out", default="profiles")
     ap.add_argument("--bench-json", default=None)
     ap.add_argument("--print-commands", action="store_true")
