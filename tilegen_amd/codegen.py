@@ -25,7 +25,8 @@ backend "hip"
         Vectorize(2) = 128-bit loads of B rows and stores of C, Unroll(u) =
         u nonzeros' B rows in flight.  With k = 64 the row is wave-uniform and
         (column, value) pairs arrive through the scalar unit.  C is written
-        exactly once per element (no read-modify-write).
+        exactly once per element (no read-modify-write), with nontemporal
+        stores since the kernel never reads it back.
     sparse_out (sddmm)
         ThreadsPerRow(k) lanes split the K-long dot product of one nonzero,
         Vectorize(2) = 128-bit loads of U and V rows, Unroll(u) = u K-chunks
@@ -33,7 +34,8 @@ backend "hip"
         rows per wave, so rows of a dense block gather the same V rows in one
         instruction), U[row, :] held in registers, column indices loaded k at
         a time and broadcast across the group, V gathers batched ahead of the
-        FMAs, one coalesced store per k outputs.  Otherwise one wave per row.
+        FMAs, one coalesced nontemporal store per k outputs (U rows, read once,
+        are nontemporal loads too).  Otherwise one wave per row.
     elementwise (axpy)
         one lane per element.
 
@@ -960,9 +962,10 @@ def _hip_row_dense_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w.close()
         if vec:
             w("tg_f64x2 c; c.x = a0; c.y = a1;")
-            w("*(tg_f64x2*)(%s + row * %s + k0) = c;" % (out_name, kext))
+            w("__builtin_nontemporal_store(c, (tg_f64x2*)(%s + row * %s + k0));"
+              % (out_name, kext))
         else:
-            w("%s[row * %s + k0] = a0;" % (out_name, kext))
+            w("__builtin_nontemporal_store(a0, %s + row * %s + k0);" % (out_name, kext))
         w.close()
 
     if V == 2:
@@ -1122,12 +1125,12 @@ def _hip_sparse_out_fast(w: _W, plan: Plan, TPR: int, U: int, V: int, SLOTS: int
     w("const tg_i64 k = (tg_i64)kq * %d + u * %d;" % (W, TPR * W))
     if W == 2:
         w.open("if (live && k < %s)" % kext)
-        w("const tg_f64x2 t = *(const tg_f64x2*)(urow + k);")
+        w("const tg_f64x2 t = __builtin_nontemporal_load((const tg_f64x2*)(urow + k));")
         w("ur[2 * u] = t.x; ur[2 * u + 1] = t.y;")
         w.close()
         w("else { ur[2 * u] = 0.0; ur[2 * u + 1] = 0.0; }")
     else:
-        w("ur[u] = (live && k < %s) ? urow[k] : 0.0;" % kext)
+        w("ur[u] = (live && k < %s) ? __builtin_nontemporal_load(urow + k) : 0.0;" % kext)
     w.close()
     w("#pragma unroll 1")
     w.open("for (tg_i64 q = 0; __builtin_amdgcn_ballot_w64(q < len) != 0; q += %d)" % TPR)
@@ -1170,7 +1173,8 @@ def _hip_sparse_out_fast(w: _W, plan: Plan, TPR: int, U: int, V: int, SLOTS: int
     w.close()
     w.close()
     env = _Env({plan.row_idx.name: "row"}, p="(rs + q + kq)", acc="res", data="dl")
-    w("if (mine) %s[rs + q + kq] = %s;" % (out_name, _cexpr(plan.final_expr, env)))
+    w("if (mine) __builtin_nontemporal_store(%s, %s + rs + q + kq);"
+      % (_cexpr(plan.final_expr, env), out_name))
     w.close()  # for q
     w.close()  # for c
     w.close()  # if fast
