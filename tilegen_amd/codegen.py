@@ -821,8 +821,8 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w.open("if (%slr < %d && row < row_end%s)" % ("lane == 0 && " if TPR > 1 else "", TR,
                                                    " && !coop[r]" if coop else ""))
     env = _Env({row: "row"}, acc="acc[r]")
-    w("%s[%s] = %s;" % (out_name, _offset(plan.out_tensor, plan.out.indices, env),
-                         _cexpr(plan.final_expr, env)))
+    w("__builtin_nontemporal_store(%s, %s + %s);" % (
+        _cexpr(plan.final_expr, env), out_name, _offset(plan.out_tensor, plan.out.indices, env)))
     w.close()
     w.close()
     if not coop:
@@ -849,8 +849,8 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w("#pragma unroll")
     w("for (int v = 0; v < %d; ++v) t += s_red[v];" % WAVES)
     env = _Env({row: "row"}, acc="t")
-    w("%s[%s] = %s;" % (out_name, _offset(plan.out_tensor, plan.out.indices, env),
-                         _cexpr(plan.final_expr, env)))
+    w("__builtin_nontemporal_store(%s, %s + %s);" % (
+        _cexpr(plan.final_expr, env), out_name, _offset(plan.out_tensor, plan.out.indices, env)))
     w.close()
     w("__syncthreads();")
     w.close()
