@@ -186,3 +186,28 @@ def test_sddmm_chunked_path(cfg, hip_ready):
     for label, A in cases.items():
         for K in (64, 40, 2):
             _check("sddmm", cfg, A, K=K, label="%s K=%d" % (label, K))
+
+
+SPMM_SKEW_CFGS = [
+    Config(tile_size=16, threads_per_row=16, unroll=2, vector_width=2, block_size=64),
+    Config(tile_size=32, threads_per_row=8, unroll=2, vector_width=2, block_size=128),
+    Config(tile_size=8, threads_per_row=64, unroll=4, vector_width=2, block_size=256),
+    Config(tile_size=256, threads_per_row=4, unroll=1, vector_width=1, block_size=1024),
+]
+
+
+@pytest.mark.parametrize("cfg", SPMM_SKEW_CFGS, ids=[schedule_id(c) for c in SPMM_SKEW_CFGS])
+def test_spmm_skewed_rows_workgroup_path(cfg, hip_ready):
+    """Rows longer than 16*U nonzeros go to the whole workgroup (strided shares,
+    fixed-order LDS tree): one enormous row, every row long, long rows at the
+    matrix end; K = 64 (128-bit path), 7 (scalar path) and 130 (several
+    K-slices)."""
+    cases = {
+        "power_law_small": make_baseline("c3a", scale=0.03),
+        "every_row_long": ragged(23, 96, 2000, 0, long_rows=[(r, 100 + 3 * r) for r in range(96)]),
+        "mixed": ragged(24, 1500, 4000, 6, empty_every=4,
+                        long_rows=[(0, 3500), (1, 17), (750, 2000), (1498, 900), (1499, 33)]),
+    }
+    for label, A in cases.items():
+        for K in (64, 7, 130):
+            _check("spmm", cfg, A, K=K, label="%s K=%d" % (label, K))

@@ -887,13 +887,22 @@ def _value_with(plan: Plan, data_text: str, gathered_text: str, row: str, col_te
 
 def _hip_row_dense_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeometry,
                        out_name: str, b_name: str, kext: str) -> None:
-    """C[row, :] = sum over nonzeros data[p] * B[col, :]; written once."""
+    """C[row, :] = sum over nonzeros data[p] * B[col, :]; written once.
+
+    Tiled variants balance long rows like SpMV does: a row longer than LONG
+    nonzeros is skipped by its lane group and listed in LDS; after the lane
+    groups' rows, every lane group of the workgroup takes a strided share of
+    each listed row's nonzeros for one K-slice at a time, and the partial
+    C-row slices are summed by a fixed LDS tree, so the result does not depend
+    on timing."""
     B, TPR = geo.block, max(1, low.threads_per_row)
     U = max(1, low.unroll)
     V = 2 if low.vector_width >= 2 else 1
     SLOTS = B // TPR
     TR = geo.rows_per_block
     R = (TR + SLOTS - 1) // SLOTS
+    LONG = 16 * U
+    coop = low.tiled
     uniform = TPR == WAVE
     w("const tg_i64 row_end = %s;" % bound)
     w("const tg_i64 row0 = (tg_i64)blockIdx.x * %d;" % TR)
@@ -906,6 +915,12 @@ def _hip_row_dense_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     if V == 2:
         w("const bool vec_ok = ((%s & 1) == 0) && ((((unsigned long long)%s) | "
           "((unsigned long long)%s)) & 15) == 0;" % (kext, b_name, out_name))
+    if coop:
+        w("__shared__ int s_long[%d];   // rows left to the whole workgroup" % TR)
+        w("__shared__ int s_nlong;")
+        w("__shared__ double s_part[%d];  // partial C-row slices, one per lane group" % (B * V))
+        w("if (threadIdx.x == 0) s_nlong = 0;")
+        w("__syncthreads();")
     w("#pragma unroll 1")
     w.open("for (int r = 0; r < %d; ++r)" % R)
     w("const int lr = slot + r * %d;" % SLOTS)
@@ -917,6 +932,11 @@ def _hip_row_dense_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     else:
         w("const tg_i64 rs = indptr[row];")
         w("const tg_i64 re = indptr[row + 1];")
+    if coop:
+        w.open("if (re - rs > %d)" % LONG)
+        w("if (lane == 0) s_long[atomicAdd(&s_nlong, 1)] = lr;")
+        w("continue;")
+        w.close()
 
     def kloop(vec: bool) -> None:
         width = 2 if vec else 1
@@ -968,15 +988,75 @@ def _hip_row_dense_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
             w("__builtin_nontemporal_store(a0, %s + row * %s + k0);" % (out_name, kext))
         w.close()
 
-    if V == 2:
-        w.open("if (vec_ok)")
-        kloop(True)
+    def both(emit) -> None:
+        if V == 2:
+            w.open("if (vec_ok)")
+            emit(True)
+            w.close()
+            w.open("else")
+            emit(False)
+            w.close()
+        else:
+            emit(False)
+
+    both(kloop)
+    w.close()
+    if not coop:
+        return
+
+    def wg_long(vec: bool) -> None:
+        width = 2 if vec else 1
+        cols = TPR * width
+        w("#pragma unroll 1")
+        w.open("for (tg_i64 kc = 0; kc < %s; kc += %d)" % (kext, cols))
+        w("const tg_i64 k0 = kc + (tg_i64)lane * %d;" % width)
+        w("const bool in_k = k0 < %s;" % kext)
+        w("double a0 = 0.0%s;" % (", a1 = 0.0" if vec else ""))
+        w("#pragma unroll 1")
+        w.open("for (tg_i64 p = crs + slot; p < cre; p += %d)" % (SLOTS * U))
+        w("tg_i64 j[%d]; double v[%d];" % (U, U))
+        w("#pragma unroll")
+        w.open("for (int u = 0; u < %d; ++u)" % U)
+        w("const tg_i64 pu = p + u * %d;" % SLOTS)
+        w("j[u] = pu < cre ? indices[pu] : 0; v[u] = pu < cre ? data[pu] : 0.0;")
         w.close()
-        w.open("else")
-        kloop(False)
+        w("#pragma unroll")
+        w.open("for (int u = 0; u < %d; ++u)" % U)
+        w.open("if (in_k && p + u * %d < cre)" % SLOTS)
+        if vec:
+            w("const tg_f64x2 b = *(const tg_f64x2*)(%s + j[u] * %s + k0);" % (b_name, kext))
+            w("a0 += v[u] * b.x; a1 += v[u] * b.y;")
+        else:
+            w("a0 += v[u] * %s[j[u] * %s + k0];" % (b_name, kext))
         w.close()
-    else:
-        kloop(False)
+        w.close()
+        w.close()
+        w("s_part[slot * %d + lane * %d] = a0;" % (cols, width))
+        if vec:
+            w("s_part[slot * %d + lane * 2 + 1] = a1;" % cols)
+        w("__syncthreads();")
+        w("// fixed-order tree over the lane groups' partial slices")
+        s_ = SLOTS // 2
+        while s_ >= 1:
+            w("for (int e = threadIdx.x; e < %d; e += %d) s_part[e] += s_part[e + %d];"
+              % (s_ * cols, B, s_ * cols))
+            w("__syncthreads();")
+            s_ //= 2
+        w.open("for (int t = threadIdx.x; t < %d; t += %d)" % (cols, B))
+        w("if (kc + t < %s) __builtin_nontemporal_store(s_part[t], %s + row * %s + kc + t);"
+          % (kext, out_name, kext))
+        w.close()
+        w("__syncthreads();")
+        w.close()
+
+    w("// long rows: every lane group takes a strided share of the row's nonzeros")
+    w("__syncthreads();")
+    w("const int n_long = s_nlong;")
+    w("#pragma unroll 1")
+    w.open("for (int kk = 0; kk < n_long; ++kk)")
+    w("const tg_i64 row = row0 + s_long[kk];")
+    w("const tg_i64 crs = indptr[row], cre = indptr[row + 1];")
+    both(wg_long)
     w.close()
 
 
