@@ -1084,7 +1084,8 @@ def _hip_sparse_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeo
     if V == 2:
         w("const bool vec_ok = ((%s & 1) == 0) && ((((unsigned long long)%s) | "
           "((unsigned long long)%s)) & 15) == 0;" % (kext, u_name, v_name))
-    _hip_sparse_out_fast(w, plan, TPR, U, V, SLOTS, WAVES, TR, out_name, u_name, v_name, kext)
+    _hip_sparse_out_fast(w, plan, TPR, U, V, SLOTS, WAVES, TR, out_name, u_name, v_name, kext,
+                         coop=low.tiled)
     w.open("else")
     w("#pragma unroll 1")
     w.open("for (int r = 0; r < %d; ++r)" % R)
@@ -1172,7 +1173,8 @@ def _sddmm_batch(TPR: int, E: int) -> int:
 
 
 def _hip_sparse_out_fast(w: _W, plan: Plan, TPR: int, U: int, V: int, SLOTS: int, WAVES: int,
-                         TR: int, out_name: str, u_name: str, v_name: str, kext: str) -> None:
+                         TR: int, out_name: str, u_name: str, v_name: str, kext: str,
+                         coop: bool = False) -> None:
     """SDDMM path for K <= TPR*V*U.  One lane group per row, SLOTS rows per
     wave, consecutive rows side by side, so rows that share columns (dense
     blocks) gather the same V rows in the same instruction.  Each lane keeps
@@ -1181,82 +1183,121 @@ def _hip_sparse_out_fast(w: _W, plan: Plan, TPR: int, U: int, V: int, SLOTS: int
     load each), the column indices are broadcast across the group with lane
     shuffles, the V-row slices of a batch are all in flight before any FMA,
     lane kq keeps the dot product of nonzero q+kq, and the chunk ends with one
-    coalesced store.  Opens an ``if``; the caller emits the general path in
-    the matching ``else``."""
+    coalesced store.  With ``coop`` (tiled variants) a row longer than 8
+    chunks is listed in LDS instead, and after the tile's other rows every
+    lane group of the workgroup takes a strided share of its chunks (SDDMM
+    outputs need no reduction across nonzeros).  Opens an ``if``; the caller
+    emits the general path in the matching ``else``."""
     W = V
     KCAP = TPR * V * U
     E = U * W
     NB = _sddmm_batch(TPR, E)
+    B = WAVES * SLOTS * TPR
+    LONG = 8 * TPR
     cond = "%s <= %d" % (kext, KCAP) + (" && vec_ok" if V == 2 else "")
+
+    def load_u(live: str) -> None:
+        w("const double* __restrict__ urow = %s + (%s ? row : 0) * %s;" % (u_name, live, kext))
+        w("double ur[%d];" % E)
+        w("#pragma unroll")
+        w.open("for (int u = 0; u < %d; ++u)" % U)
+        w("const tg_i64 k = (tg_i64)kq * %d + u * %d;" % (W, TPR * W))
+        if W == 2:
+            w.open("if (%s && k < %s)" % (live, kext))
+            w("const tg_f64x2 t = __builtin_nontemporal_load((const tg_f64x2*)(urow + k));")
+            w("ur[2 * u] = t.x; ur[2 * u + 1] = t.y;")
+            w.close()
+            w("else { ur[2 * u] = 0.0; ur[2 * u + 1] = 0.0; }")
+        else:
+            w("ur[u] = (%s && k < %s) ? __builtin_nontemporal_load(urow + k) : 0.0;"
+              % (live, kext))
+        w.close()
+
+    def chunks(q0: str, step: int) -> None:
+        """Chunks of TPR nonzeros of [rs, rs + len) starting at q0, every step."""
+        w("#pragma unroll 1")
+        w.open("for (tg_i64 q = %s; __builtin_amdgcn_ballot_w64(q < len) != 0; q += %d)"
+               % (q0, step))
+        w("const bool mine = q + kq < len;")
+        w("const tg_i64 jl = mine ? indices[rs + q + kq] : 0;")
+        w("const double dl = mine ? data[rs + q + kq] : 0.0;")
+        w("double res = 0.0;")
+        w("#pragma unroll")
+        w.open("for (int n0 = 0; n0 < %d; n0 += %d)" % (TPR, NB))
+        w("double x[%d][%d];" % (NB, E))
+        w("#pragma unroll")
+        w.open("for (int n = 0; n < %d; ++n)" % NB)
+        if TPR > 1:
+            w("const tg_i64 j = tg_lane_bcast(jl, slot * %d + n0 + n);" % TPR)
+        else:
+            w("const tg_i64 j = jl;")
+        w("const bool v = q + n0 + n < len;")
+        w("const double* __restrict__ vr = %s + j * %s;" % (v_name, kext))
+        w("#pragma unroll")
+        w.open("for (int u = 0; u < %d; ++u)" % U)
+        w("const tg_i64 k = (tg_i64)kq * %d + u * %d;" % (W, TPR * W))
+        if W == 2:
+            w.open("if (v && k < %s)" % kext)
+            w("const tg_f64x2 t = *(const tg_f64x2*)(vr + k);")
+            w("x[n][2 * u] = t.x; x[n][2 * u + 1] = t.y;")
+            w.close()
+            w("else { x[n][2 * u] = 0.0; x[n][2 * u + 1] = 0.0; }")
+        else:
+            w("x[n][u] = (v && k < %s) ? vr[k] : 0.0;" % kext)
+        w.close()
+        w.close()
+        w("#pragma unroll")
+        w.open("for (int n = 0; n < %d; ++n)" % NB)
+        w("double acc = 0.0;")
+        w("#pragma unroll")
+        w("for (int e = 0; e < %d; ++e) acc += ur[e] * x[n][e];" % E)
+        if TPR > 1:
+            w("acc = tg_segsum<%d>(acc);" % TPR)
+        w("if (kq == n0 + n) res = acc;")
+        w.close()
+        w.close()
+        env = _Env({plan.row_idx.name: "row"}, p="(rs + q + kq)", acc="res", data="dl")
+        w("if (mine) __builtin_nontemporal_store(%s, %s + rs + q + kq);"
+          % (_cexpr(plan.final_expr, env), out_name))
+        w.close()
+
     w.open("if (%s)" % cond)
     w("// one lane group per row; chunks of %d nonzeros, V slices gathered %d at a time"
       % (TPR, NB))
+    if coop:
+        w("__shared__ int s_long[%d];   // rows left to the whole workgroup" % TR)
+        w("__shared__ int s_nlong;")
+        w("if (threadIdx.x == 0) s_nlong = 0;")
+        w("__syncthreads();")
     w("#pragma unroll 1")
     w.open("for (int c = wave; c * %d < %d; c += %d)" % (SLOTS, TR, WAVES))
     w("const int lr = c * %d + slot;" % SLOTS)
     w("const tg_i64 row = row0 + lr;")
     w("const bool live = lr < %d && row < row_end;" % TR)
     w("const tg_i64 rs = live ? indptr[row] : 0;")
-    w("const tg_i64 len = live ? indptr[row + 1] - rs : 0;")
-    w("const double* __restrict__ urow = %s + (live ? row : 0) * %s;" % (u_name, kext))
-    w("double ur[%d];" % E)
-    w("#pragma unroll")
-    w.open("for (int u = 0; u < %d; ++u)" % U)
-    w("const tg_i64 k = (tg_i64)kq * %d + u * %d;" % (W, TPR * W))
-    if W == 2:
-        w.open("if (live && k < %s)" % kext)
-        w("const tg_f64x2 t = __builtin_nontemporal_load((const tg_f64x2*)(urow + k));")
-        w("ur[2 * u] = t.x; ur[2 * u + 1] = t.y;")
+    if coop:
+        w("tg_i64 len = live ? indptr[row + 1] - rs : 0;")
+        w.open("if (len > %d)" % LONG)
+        w("if (kq == 0) s_long[atomicAdd(&s_nlong, 1)] = lr;")
+        w("len = 0;  // the lane group skips it")
         w.close()
-        w("else { ur[2 * u] = 0.0; ur[2 * u + 1] = 0.0; }")
     else:
-        w("ur[u] = (live && k < %s) ? __builtin_nontemporal_load(urow + k) : 0.0;" % kext)
-    w.close()
-    w("#pragma unroll 1")
-    w.open("for (tg_i64 q = 0; __builtin_amdgcn_ballot_w64(q < len) != 0; q += %d)" % TPR)
-    w("const bool mine = q + kq < len;")
-    w("const tg_i64 jl = mine ? indices[rs + q + kq] : 0;")
-    w("const double dl = mine ? data[rs + q + kq] : 0.0;")
-    w("double res = 0.0;")
-    w("#pragma unroll")
-    w.open("for (int n0 = 0; n0 < %d; n0 += %d)" % (TPR, NB))
-    w("double x[%d][%d];" % (NB, E))
-    w("#pragma unroll")
-    w.open("for (int n = 0; n < %d; ++n)" % NB)
-    if TPR > 1:
-        w("const tg_i64 j = tg_lane_bcast(jl, slot * %d + n0 + n);" % TPR)
-    else:
-        w("const tg_i64 j = jl;")
-    w("const bool v = q + n0 + n < len;")
-    w("const double* __restrict__ vr = %s + j * %s;" % (v_name, kext))
-    w("#pragma unroll")
-    w.open("for (int u = 0; u < %d; ++u)" % U)
-    w("const tg_i64 k = (tg_i64)kq * %d + u * %d;" % (W, TPR * W))
-    if W == 2:
-        w.open("if (v && k < %s)" % kext)
-        w("const tg_f64x2 t = *(const tg_f64x2*)(vr + k);")
-        w("x[n][2 * u] = t.x; x[n][2 * u + 1] = t.y;")
-        w.close()
-        w("else { x[n][2 * u] = 0.0; x[n][2 * u + 1] = 0.0; }")
-    else:
-        w("x[n][u] = (v && k < %s) ? vr[k] : 0.0;" % kext)
-    w.close()
-    w.close()
-    w("#pragma unroll")
-    w.open("for (int n = 0; n < %d; ++n)" % NB)
-    w("double acc = 0.0;")
-    w("#pragma unroll")
-    w("for (int e = 0; e < %d; ++e) acc += ur[e] * x[n][e];" % E)
-    if TPR > 1:
-        w("acc = tg_segsum<%d>(acc);" % TPR)
-    w("if (kq == n0 + n) res = acc;")
-    w.close()
-    w.close()
-    env = _Env({plan.row_idx.name: "row"}, p="(rs + q + kq)", acc="res", data="dl")
-    w("if (mine) __builtin_nontemporal_store(%s, %s + rs + q + kq);"
-      % (_cexpr(plan.final_expr, env), out_name))
-    w.close()  # for q
+        w("const tg_i64 len = live ? indptr[row + 1] - rs : 0;")
+    load_u("live")
+    chunks("0", TPR)
     w.close()  # for c
+    if coop:
+        w("// long rows: every lane group of the workgroup takes a strided share of the chunks")
+        w("__syncthreads();")
+        w("const int n_long = s_nlong;")
+        w("#pragma unroll 1")
+        w.open("for (int kk = 0; kk < n_long; ++kk)")
+        w("const tg_i64 row = row0 + s_long[kk];")
+        w("const tg_i64 rs = indptr[row];")
+        w("const tg_i64 len = indptr[row + 1] - rs;")
+        load_u("true")
+        chunks("(tg_i64)(wave * %d + slot) * %d" % (SLOTS, TPR), B)
+        w.close()
     w.close()  # if fast
 
 
