@@ -167,7 +167,10 @@ def test_hip_no_reduction_when_one_lane_per_row():
 def test_hip_long_rows_go_to_the_workgroup_only_when_tiled():
     cfg = Config(tile_size=64, threads_per_row=4, unroll=2, block_size=256)
     tiled = _hip("spmv", cfg)
-    assert "coop[r] = re[r] - rs[r] > 64;" in tiled  # 8 steps of 4 lanes x 2 nonzeros
+    # past 8 steps of 4 lanes x 2 nonzeros, and either 2x the tile's average
+    # row or past 16 steps
+    assert ("coop[r] = ((re[r] - rs[r]) > 64 && ((re[r] - rs[r]) * t_rows > 2 * t_nnz || "
+            "(re[r] - rs[r]) > 128));") in tiled
     assert "s_long[atomicAdd(&s_nlong, 1)] = lr;" in tiled
     assert "s_long[" not in _hip("spmv", cfg, skip=("tiling",))
 

@@ -691,6 +691,30 @@ def _check_hip_schedule(plan: Plan, low: Lowering) -> None:
         raise ValueError("tile_size %d exceeds 4096 rows per workgroup" % low.tile)
 
 
+def _long_row_test(length: str, long_: int, huge: int) -> str:
+    """Whether a row leaves its lane group for the whole workgroup: longer than
+    ``long_`` and either more than 2x the tile's average row or longer than
+    ``huge``.  Rows that are uniformly long stay with their lane groups, which
+    keep every group equally busy; a row that dwarfs its tile, or one so long
+    that one lane group would walk it for too many steps, is shared."""
+    n = "(%s)" % length
+    return "(%s > %d && (%s * t_rows > 2 * t_nnz || %s > %d))" % (n, long_, n, n, huge)
+
+
+def _tile_stats(w: _W, TR: int) -> None:
+    """t_rows / t_nnz of this workgroup's tile (rows and nonzeros), and a
+    zeroed long-row count; ends with a barrier."""
+    w("__shared__ tg_i64 s_tnnz;")
+    w.open("if (threadIdx.x == 0)")
+    w("s_nlong = 0;")
+    w("const tg_i64 t_end = row0 + %d < row_end ? row0 + %d : row_end;" % (TR, TR))
+    w("s_tnnz = t_end > row0 ? indptr[t_end] - indptr[row0] : 0;")
+    w.close()
+    w("__syncthreads();")
+    w("const tg_i64 t_rows = row_end - row0 < %d ? row_end - row0 : %d;" % (TR, TR))
+    w("const tg_i64 t_nnz = s_tnnz;")
+
+
 def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeometry,
                        out_name: str) -> None:
     """y[row] = final(sum over the row's nonzeros of value_expr).
@@ -708,7 +732,8 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     R = (TR + SLOTS - 1) // SLOTS
     ALIGN = 2 if U % 2 == 0 else 1
     STEP = TPR * U
-    LONG = 8 * STEP
+    LONG = 8 * STEP    # longer rows may leave their lane group ...
+    HUGE = 16 * STEP   # ... and always do past this length
     WAVES = B // WAVE
     coop = low.tiled
     row = plan.row_idx.name
@@ -730,6 +755,8 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("s_ptr[t] = indptr[r < row_end ? r : row_end];")
         w.close()
         w("__syncthreads();")
+        w("const tg_i64 t_rows = row_end - row0 < %d ? row_end - row0 : %d;" % (TR, TR))
+        w("const tg_i64 t_nnz = s_ptr[%d] - s_ptr[0];" % TR)
     w("tg_i64 rs[%d], re[%d];" % (R, R))
     w("double acc[%d];" % R)
     if coop:
@@ -747,7 +774,7 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("rs[r] = live ? indptr[ri] : 0;")
         w("re[r] = live ? indptr[ri + 1] : 0;")
     if coop:
-        w("coop[r] = re[r] - rs[r] > %d;" % LONG)
+        w("coop[r] = %s;" % _long_row_test("re[r] - rs[r]", LONG, HUGE))
         w.open("if (coop[r])")
         w("if (lane == 0) s_long[atomicAdd(&s_nlong, 1)] = lr;")
         w("re[r] = rs[r];  // the lane group skips it")
@@ -901,7 +928,8 @@ def _hip_row_dense_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     SLOTS = B // TPR
     TR = geo.rows_per_block
     R = (TR + SLOTS - 1) // SLOTS
-    LONG = 16 * U
+    LONG = 16 * U     # longer rows may leave their lane group ...
+    HUGE = 64 * U     # ... and always do past this length
     coop = low.tiled
     uniform = TPR == WAVE
     w("const tg_i64 row_end = %s;" % bound)
@@ -919,8 +947,7 @@ def _hip_row_dense_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("__shared__ int s_long[%d];   // rows left to the whole workgroup" % TR)
         w("__shared__ int s_nlong;")
         w("__shared__ double s_part[%d];  // partial C-row slices, one per lane group" % (B * V))
-        w("if (threadIdx.x == 0) s_nlong = 0;")
-        w("__syncthreads();")
+        _tile_stats(w, TR)
     w("#pragma unroll 1")
     w.open("for (int r = 0; r < %d; ++r)" % R)
     w("const int lr = slot + r * %d;" % SLOTS)
@@ -933,7 +960,7 @@ def _hip_row_dense_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("const tg_i64 rs = indptr[row];")
         w("const tg_i64 re = indptr[row + 1];")
     if coop:
-        w.open("if (re - rs > %d)" % LONG)
+        w.open("if (%s)" % _long_row_test("re - rs", LONG, HUGE))
         w("if (lane == 0) s_long[atomicAdd(&s_nlong, 1)] = lr;")
         w("continue;")
         w.close()
@@ -1193,7 +1220,8 @@ def _hip_sparse_out_fast(w: _W, plan: Plan, TPR: int, U: int, V: int, SLOTS: int
     E = U * W
     NB = _sddmm_batch(TPR, E)
     B = WAVES * SLOTS * TPR
-    LONG = 8 * TPR
+    LONG = 8 * TPR     # longer rows may leave their lane group ...
+    HUGE = 16 * TPR    # ... and always do past this length
     cond = "%s <= %d" % (kext, KCAP) + (" && vec_ok" if V == 2 else "")
 
     def load_u(live: str) -> None:
@@ -1267,8 +1295,7 @@ def _hip_sparse_out_fast(w: _W, plan: Plan, TPR: int, U: int, V: int, SLOTS: int
     if coop:
         w("__shared__ int s_long[%d];   // rows left to the whole workgroup" % TR)
         w("__shared__ int s_nlong;")
-        w("if (threadIdx.x == 0) s_nlong = 0;")
-        w("__syncthreads();")
+        _tile_stats(w, TR)
     w("#pragma unroll 1")
     w.open("for (int c = wave; c * %d < %d; c += %d)" % (SLOTS, TR, WAVES))
     w("const int lr = c * %d + slot;" % SLOTS)
@@ -1277,7 +1304,7 @@ def _hip_sparse_out_fast(w: _W, plan: Plan, TPR: int, U: int, V: int, SLOTS: int
     w("const tg_i64 rs = live ? indptr[row] : 0;")
     if coop:
         w("tg_i64 len = live ? indptr[row + 1] - rs : 0;")
-        w.open("if (len > %d)" % LONG)
+        w.open("if (%s)" % _long_row_test("len", LONG, HUGE))
         w("if (kq == 0) s_long[atomicAdd(&s_nlong, 1)] = lr;")
         w("len = 0;  // the lane group skips it")
         w.close()
