@@ -167,10 +167,7 @@ def test_hip_no_reduction_when_one_lane_per_row():
 def test_hip_long_rows_go_to_the_workgroup_only_when_tiled():
     cfg = Config(tile_size=64, threads_per_row=4, unroll=2, block_size=256)
     tiled = _hip("spmv", cfg)
-    # past 8 steps of 4 lanes x 2 nonzeros, and either 2x the tile's average
-    # row or past 16 steps
-    assert ("coop[r] = ((re[r] - rs[r]) > 64 && ((re[r] - rs[r]) * t_rows > 2 * t_nnz || "
-            "(re[r] - rs[r]) > 128));") in tiled
+    assert "coop[r] = re[r] - rs[r] > 64;" in tiled  # 8 steps of 4 lanes x 2 nonzeros
     assert "s_long[atomicAdd(&s_nlong, 1)] = lr;" in tiled
     assert "s_long[" not in _hip("spmv", cfg, skip=("tiling",))
 
@@ -295,3 +292,17 @@ def test_cpu_simd_pragma_sits_on_its_loop():
     lines = [l.strip() for l in src.splitlines()]
     i = lines.index("#pragma omp simd")
     assert lines[i + 1].startswith("for (")
+
+
+def test_spmm_sddmm_long_rows_relative_to_the_tile():
+    """SpMM/SDDMM share a row with the workgroup only when it dwarfs its tile
+    (more than 2x the average row) or is long outright; uniformly long rows
+    stay with their lane groups."""
+    spmm = _hip("spmm", Config(tile_size=16, threads_per_row=16, unroll=2, vector_width=2,
+                               block_size=64))
+    assert "((re - rs) > 32 && ((re - rs) * t_rows > 2 * t_nnz || (re - rs) > 128))" in spmm
+    sddmm = _hip("sddmm", Config(tile_size=16, threads_per_row=8, unroll=4, vector_width=2,
+                                 block_size=128))
+    assert "((len) > 64 && ((len) * t_rows > 2 * t_nnz || (len) > 128))" in sddmm
+    assert "s_tnnz = t_end > row0 ? indptr[t_end] - indptr[row0] : 0;" in sddmm
+

@@ -732,8 +732,7 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     R = (TR + SLOTS - 1) // SLOTS
     ALIGN = 2 if U % 2 == 0 else 1
     STEP = TPR * U
-    LONG = 8 * STEP    # longer rows may leave their lane group ...
-    HUGE = 16 * STEP   # ... and always do past this length
+    LONG = 8 * STEP    # longer rows leave their lane group
     WAVES = B // WAVE
     coop = low.tiled
     row = plan.row_idx.name
@@ -755,8 +754,6 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("s_ptr[t] = indptr[r < row_end ? r : row_end];")
         w.close()
         w("__syncthreads();")
-        w("const tg_i64 t_rows = row_end - row0 < %d ? row_end - row0 : %d;" % (TR, TR))
-        w("const tg_i64 t_nnz = s_ptr[%d] - s_ptr[0];" % TR)
     w("tg_i64 rs[%d], re[%d];" % (R, R))
     w("double acc[%d];" % R)
     if coop:
@@ -774,7 +771,7 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("rs[r] = live ? indptr[ri] : 0;")
         w("re[r] = live ? indptr[ri + 1] : 0;")
     if coop:
-        w("coop[r] = %s;" % _long_row_test("re[r] - rs[r]", LONG, HUGE))
+        w("coop[r] = re[r] - rs[r] > %d;" % LONG)
         w.open("if (coop[r])")
         w("if (lane == 0) s_long[atomicAdd(&s_nlong, 1)] = lr;")
         w("re[r] = rs[r];  // the lane group skips it")
