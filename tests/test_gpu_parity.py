@@ -211,3 +211,24 @@ def test_spmm_skewed_rows_workgroup_path(cfg, hip_ready):
     for label, A in cases.items():
         for K in (64, 7, 130):
             _check("spmm", cfg, A, K=K, label="%s K=%d" % (label, K))
+
+
+SDDMM_WIDE_CFGS = [
+    Config(tile_size=16, threads_per_row=4, unroll=2, vector_width=2, block_size=256),
+    Config(tile_size=8, threads_per_row=16, unroll=1, vector_width=1, block_size=128),
+    Config(tile_size=64, threads_per_row=64, unroll=2, vector_width=2, block_size=1024),
+]
+
+
+@pytest.mark.parametrize("cfg", SDDMM_WIDE_CFGS, ids=[schedule_id(c) for c in SDDMM_WIDE_CFGS])
+def test_sddmm_wide_k_skewed_rows(cfg, hip_ready):
+    """K wider than one lane group's registers (one wave per row): rows that
+    dwarf their tile are shared by every wave of the workgroup."""
+    cases = {
+        "power_law_small": make_baseline("c3a", scale=0.03),
+        "mixed": ragged(25, 1200, 3000, 5, empty_every=4,
+                        long_rows=[(0, 2500), (1, 300), (600, 1200), (1199, 700)]),
+    }
+    for label, A in cases.items():
+        for K in (130, 257):
+            _check("sddmm", cfg, A, K=K, label="%s K=%d" % (label, K))

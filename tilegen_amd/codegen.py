@@ -1111,21 +1111,9 @@ def _hip_sparse_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeo
     _hip_sparse_out_fast(w, plan, TPR, U, V, SLOTS, WAVES, TR, out_name, u_name, v_name, kext,
                          coop=low.tiled)
     w.open("else")
-    w("#pragma unroll 1")
-    w.open("for (int r = 0; r < %d; ++r)" % R)
-    w("const int lr = wave + r * %d;" % WAVES)
-    w("const tg_i64 row = row0 + lr;")
-    w("if (lr >= %d || row >= row_end) break;" % TR)
-    w("const tg_i64 rs = tg_uniform(indptr[row]);")
-    w("const tg_i64 re = tg_uniform(indptr[row + 1]);")
-    w("const double* __restrict__ urow = %s + row * %s;" % (u_name, kext))
-    w("#pragma unroll 1")
-    w.open("for (tg_i64 p0 = rs; p0 < re; p0 += %d)" % SLOTS)
-    w("const tg_i64 p = p0 + slot;")
-    w("const bool valid = p < re;")
-    w("double acc = 0.0;")
-    w.open("if (valid)")
-    w("const double* __restrict__ vrow = %s + indices[p] * %s;" % (v_name, kext))
+    coop = low.tiled
+    LONG = 8 * SLOTS   # 8 wave steps ...
+    HUGE = 16 * SLOTS
 
     def kloop(vec: bool) -> None:
         width = 2 if vec else 1
@@ -1165,24 +1153,64 @@ def _hip_sparse_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeo
             w("acc += urow[k] * vrow[k];")
         w.close()
 
-    if V == 2:
-        w.open("if (vec_ok)")
-        kloop(True)
+    def row_body(p_start: str, p_step: int) -> None:
+        """The row's nonzeros from p_start every p_step, SLOTS at a time, each
+        lane group looping over K."""
+        w("const double* __restrict__ urow = %s + row * %s;" % (u_name, kext))
+        w("#pragma unroll 1")
+        w.open("for (tg_i64 p0 = %s; p0 < re; p0 += %d)" % (p_start, p_step))
+        w("const tg_i64 p = p0 + slot;")
+        w("const bool valid = p < re;")
+        w("double acc = 0.0;")
+        w.open("if (valid)")
+        w("const double* __restrict__ vrow = %s + indices[p] * %s;" % (v_name, kext))
+        if V == 2:
+            w.open("if (vec_ok)")
+            kloop(True)
+            w.close()
+            w.open("else")
+            kloop(False)
+            w.close()
+        else:
+            kloop(False)
         w.close()
-        w.open("else")
-        kloop(False)
+        if TPR > 1:
+            w("acc = tg_segsum<%d>(acc);" % TPR)
+        env = _Env({plan.row_idx.name: "row"}, p="p", acc="acc")
+        w.open("if (valid%s)" % (" && kq == 0" if TPR > 1 else ""))
+        w("%s[p] = %s;" % (out_name, _cexpr(plan.final_expr, env)))
         w.close()
-    else:
-        kloop(False)
-    w.close()
-    if TPR > 1:
-        w("acc = tg_segsum<%d>(acc);" % TPR)
-    env = _Env({plan.row_idx.name: "row"}, p="p", acc="acc")
-    w.open("if (valid%s)" % (" && kq == 0" if TPR > 1 else ""))
-    w("%s[p] = %s;" % (out_name, _cexpr(plan.final_expr, env)))
-    w.close()
-    w.close()
+        w.close()
+
+    if coop:
+        w("__shared__ int s_long[%d];   // rows left to every wave of the workgroup" % TR)
+        w("__shared__ int s_nlong;")
+        _tile_stats(w, TR)
+    w("#pragma unroll 1")
+    w.open("for (int r = 0; r < %d; ++r)" % R)
+    w("const int lr = wave + r * %d;" % WAVES)
+    w("const tg_i64 row = row0 + lr;")
+    w("if (lr >= %d || row >= row_end) break;" % TR)
+    w("const tg_i64 rs = tg_uniform(indptr[row]);")
+    w("const tg_i64 re = tg_uniform(indptr[row + 1]);")
+    if coop:
+        w.open("if (%s)" % _long_row_test("re - rs", LONG, HUGE))
+        w("if (wl == 0) s_long[atomicAdd(&s_nlong, 1)] = lr;")
+        w("continue;")
+        w.close()
+    row_body("rs", SLOTS)
     w.close()  # for r
+    if coop:
+        w("// long rows: every wave of the workgroup takes every %d-th step" % WAVES)
+        w("__syncthreads();")
+        w("const int n_long = s_nlong;")
+        w("#pragma unroll 1")
+        w.open("for (int kk = 0; kk < n_long; ++kk)")
+        w("const tg_i64 row = row0 + s_long[kk];")
+        w("const tg_i64 rs = tg_uniform(indptr[row]);")
+        w("const tg_i64 re = tg_uniform(indptr[row + 1]);")
+        row_body("rs + (tg_i64)wave * %d" % SLOTS, WAVES * SLOTS)
+        w.close()
     w.close()  # else (general path)
 
 
