@@ -10,6 +10,16 @@ Modules keep the reference's names and entry points:
     matrices          reference corpus and the BASELINE inputs
     env               toolchain / GPU probe
     runtime           ctypes binding of libtgrt (include/tgrt.h)
+
+Around them (the reference's scripts/ and harness, rebuilt for this backend):
+    variant           one compiled variant: launch, geometry, timing handles
+    schedules         tuned schedule per BASELINE case, test schedules
+    verify_all        every kernel x schedule x corpus class, injected bugs
+    tune_all          corpus autotune into results/
+    ablation          per-pass contribution (code diff, verify, GPU timing)
+    vendor            rocSPARSE SpMV timing beside the tuned kernel
+    profiling         rocprofv3 summaries for profiles/
+    build             in-tree native build (libtgrt, harness, oracle, kernel cache)
 """
 
 __version__ = "0.1.0"
