@@ -32,7 +32,7 @@ from typing import Dict, List, Optional
 
 import numpy as np
 
-__all__ = ["commands", "trace_stats", "pmc_values", "summarize"]
+__all__ = ["commands", "trace_stats", "pmc_values", "summarize", "valu_command", "valu_summary"]
 
 COPY_MIB = 256
 BENCH_PMC = "python3 bench.py --case {case} --no-cpu --steps 20 --warmup 2"
@@ -54,6 +54,16 @@ def commands(case: str, root: str = "rocprof_out") -> Dict[str, str]:
         "copy_write": "rocprofv3 --pmc WRITE_SIZE --output-format csv -d %s/copy_write -o pmc "
                       "-- python3 bench.py --calibrate-copy %d" % (root, COPY_MIB),
     }
+
+
+VALU_COUNTERS = ("SQ_INSTS_VALU SQ_ACTIVE_INST_VALU SQ_BUSY_CU_CYCLES SQ_WAVE_CYCLES "
+                 "SQ_INSTS_VALU_FMA_F64 SQ_INSTS_VALU_FLOPS_FP64 GRBM_GUI_ACTIVE")
+
+
+def valu_command(case: str, root: str = "rocprof_out") -> str:
+    """One PMC pass with the VALU counters (7 counters: 6 SQ, 1 GRBM)."""
+    return ("rocprofv3 --pmc %s --output-format csv -d %s/%s/valu -o pmc -- %s"
+            % (VALU_COUNTERS, root, case, BENCH_PMC.format(case=case)))
 
 
 def _find(d: str, suffix: str) -> Optional[str]:
@@ -185,6 +195,62 @@ def summarize(case: str, root: str, out_dir: str, bench_json: Optional[str] = No
     return summary
 
 
+def valu_summary(case: str, root: str, out_dir: str, bench_json: Optional[str] = None
+                 ) -> Dict[str, object]:
+    """profiles/<kernel>_<case>_valu.md: vector-ALU activity of the kernel, the
+    evidence for whether a matrix-core (MFMA) formulation could help it."""
+    from .matrices import baseline_case, flops, make_baseline
+    bc = baseline_case(case)
+    kernel = "%s_kernel" % bc.kernel
+    d = os.path.join(root, case, "valu")
+    med = {c: float(np.median(pmc_values(d, kernel, c))) for c in VALU_COUNTERS.split()}
+    A = make_baseline(case)
+    alg_flops = flops(bc.kernel, int(A.nnz), bc.K)
+    us = None
+    if bench_json and os.path.exists(bench_json):
+        with open(bench_json) as fh:
+            lines = [l for l in fh.read().splitlines() if l.startswith("{")]
+        us = json.loads(lines[-1])["kernel_us_avg"] if lines else None
+    # MI355X: 256 CUs x 4 SIMDs at up to 2.4 GHz; a wave64 fp64 FMA occupies a
+    # SIMD for 4 cycles (78.6 TFLOP/s = 1024 SIMDs x 2.4 GHz x 16 lanes x 2).
+    simd_cycles = 1024 * 2.4e9 * us * 1e-6 if us else None
+    fma_share = (4.0 * med["SQ_INSTS_VALU_FMA_F64"] / simd_cycles) if simd_cycles else None
+    valu_share = (med["SQ_INSTS_VALU"] / simd_cycles) if simd_cycles else None
+    summary = {"case": case, "kernel": kernel, "counters": med, "algorithmic_flops": alg_flops,
+               "kernel_us_avg": us, "fp64_fma_simd_share": fma_share,
+               "valu_issue_share_lower_bound": valu_share,
+               "fp64_tflops_achieved": (alg_flops / (us * 1e-6) / 1e12) if us else None,
+               "fp64_tflops_peak": 78.6, "command": valu_command(case, root)}
+    os.makedirs(out_dir, exist_ok=True)
+    stem = os.path.join(out_dir, "%s_%s_valu" % (bc.kernel, case))
+    with open(stem + ".json", "w") as fh:
+        json.dump(summary, fh, indent=1)
+    rows = ["| %s | %.4g |" % (c, med[c]) for c in VALU_COUNTERS.split()]
+    text = [
+        "# Vector-ALU activity of %s on %s" % (kernel, case), "",
+        "| counter (median per dispatch) | value |", "|---|---:|"] + rows + [
+        "",
+        "Algorithmic fp64 work: %.4g flop per launch%s." % (
+            alg_flops, (", %.2f TFLOP/s at the bench's %.2f µs kernel average (fp64 vector "
+                        "peak 78.6)" % (summary["fp64_tflops_achieved"], us)) if us else ""),
+        "SQ_INSTS_VALU_FMA_F64 counts wave64 fp64 FMA instructions; algorithmic flops / 128 = "
+        "%.4g." % (alg_flops / 128.0),
+        "Share of SIMD time (1024 SIMDs x 2.4 GHz x kernel time) the fp64 FMAs occupy at 4 "
+        "cycles each: %s; all VALU instructions at one cycle each: %s. Only the FMA share is "
+        "work a matrix-core formulation could take over." % (
+            "%.3f" % fma_share if fma_share is not None else "n/a",
+            "%.3f" % valu_share if valu_share is not None else "n/a"),
+        "",
+        "## Command (from the repository root on the GPU box)", "",
+        "    " + valu_command(case, root), "",
+        "Summary written by `python -m tilegen_amd.profiling --case %s --root %s --valu`."
+        % (case, root),
+    ]
+    with open(stem + ".md", "w") as fh:
+        fh.write("\n".join(text) + "\n")
+    return summary
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="Summarize rocprofv3 CSV output into profiles/.")
     ap.add_argument("--case", required=True)
@@ -192,7 +258,15 @@ def main(argv=None) -> int:
     ap.add_argument("--out", default="profiles")
     ap.add_argument("--bench-json", default=None)
     ap.add_argument("--print-commands", action="store_true")
+    ap.add_argument("--valu", action="store_true",
+                    help="summarize the VALU counter pass (valu_command) instead")
     a = ap.parse_args(argv)
+    if a.valu:
+        v = valu_summary(a.case, a.root, a.out, a.bench_json)
+        print(json.dumps({k: v[k] for k in ("case", "fp64_fma_simd_share",
+                                             "valu_issue_share_lower_bound",
+                                             "fp64_tflops_achieved")}))
+        return 0
     if a.print_commands:
         for c in commands(a.case, a.root).values():
             print(c)
