@@ -179,8 +179,9 @@ def main(argv=None) -> int:
     ap.add_argument("--warm", action="store_true",
                     help="no input rotation (cache-warm figure, reported as such)")
     ap.add_argument("--vendor", default=None, metavar="ALG",
-                    help="also time rocSPARSE SpMV (adaptive|rowsplit|lrb|nnzsplit) on the "
-                         "same rotated inputs; reported as an extra field")
+                    help="also time rocSPARSE on the same rotated inputs, reported as an extra "
+                         "field: spmv adaptive|rowsplit|lrb|nnzsplit, spmm "
+                         "default|csr|row_split|nnz_split|merge_path, sddmm default")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only launch a plain copy of MIB MiB (PMC byte-count calibration)")
     args = ap.parse_args(argv)
@@ -272,19 +273,35 @@ def main(argv=None) -> int:
                                         ev_wall_ms / args.steps))
 
     vendor = None
-    if args.vendor and case.kernel == "spmv":
+    if args.vendor:
         from tilegen_amd import vendor as vd
-        vsets = [[b["indptr"], b["indices"], b["data"], b["x"], b["y"]] for b in keep]
-        vms, vwall = vd.spmv_time(args.vendor, M, N, nnz, vsets, args.warmup, args.steps)
-        vgot = keep[0]["y"].to_host()
-        verr = float(np.abs(vgot - ref).max() / max(np.abs(ref).max(), 1e-300))
+        out_key = {"spmv": "y", "spmm": "C", "sddmm": "C"}[case.kernel]
+        for b in keep:  # the vendor call writes the same output buffers
+            b[out_key].upload(np.zeros(out_shape))
+        if case.kernel == "spmv":
+            vsets = [[b["indptr"], b["indices"], b["data"], b["x"], b["y"]] for b in keep]
+            vms, _ = vd.spmv_time(args.vendor, M, N, nnz, vsets, args.warmup, args.steps)
+            vref, call = ref, "rocsparse_spmv compute call"
+        elif case.kernel == "spmm":
+            vsets = [[b["indptr"], b["indices"], b["data"], b["B"], b["C"]] for b in keep]
+            vms, _ = vd.spmm_time(args.vendor, M, N, K, nnz, vsets, args.warmup, args.steps)
+            vref, call = ref, "rocsparse_spmm compute call"
+        else:
+            vsets = [[b["indptr"], b["indices"], b["U"], b["V"], b["C"]] for b in keep]
+            vms, _ = vd.sddmm_time(args.vendor, M, N, K, nnz, vsets, args.warmup, args.steps)
+            # rocSPARSE's SDDMM does not multiply by A's values
+            coo = A.tocoo()
+            vref = np.einsum("ik,ik->i", ops["U"][coo.row], ops["V"][coo.col])
+            call = "rocsparse_sddmm call (no multiply by A's values)"
+        vgot = keep[0][out_key].to_host().reshape(np.shape(vref))
+        verr = float(np.abs(vgot - vref).max() / max(np.abs(vref).max(), 1e-300))
         vmed = float(np.median(vms)) * 1e-3
         vendor = {"library": "rocSPARSE", "alg": args.vendor, "us_median": round(vmed * 1e6, 3),
                   "gbs_median": round(nbytes / vmed / 1e9, 2),
-                  "timer": "hipEvents around each rocsparse_spmv compute call",
-                  "rel_err": verr}
-        _log("rocSPARSE %s: median %.2f us per call (%.0f GB/s), rel err %.2e" % (
-            args.vendor, vmed * 1e6, nbytes / vmed / 1e9, verr))
+                  "gflops_median": round(nflop / vmed / 1e9, 2),
+                  "timer": "hipEvents around each " + call, "rel_err": verr}
+        _log("rocSPARSE %s: median %.2f us per call (%.0f GB/s, %.0f GFLOP/s), rel err %.2e" % (
+            args.vendor, vmed * 1e6, nbytes / vmed / 1e9, nflop / vmed / 1e9, verr))
 
     cpu = None
     if not args.no_cpu:
