@@ -140,7 +140,10 @@ def _compile_hip(gen: "_codegen.GeneratedKernel", workdir: str) -> Tuple[str, st
     host = gen.host_source.replace("{CODE_SIZE}", str(len(code))).replace(
         "{CODE_OBJECT}", _bytes_as_c(code))
     os.makedirs(workdir, exist_ok=True)
-    host_src = os.path.join(workdir, gen.filename.rsplit(".", 1)[0] + "_launch.c")
+    # per-process file name: concurrent builds of one variant never read a
+    # launcher source another process is still writing
+    host_src = os.path.join(workdir, "%s_launch.%d.c" % (gen.filename.rsplit(".", 1)[0],
+                                                          os.getpid()))
     with open(host_src, "w") as fh:
         fh.write(host)
     libdir = _rt.lib_dir()
