@@ -1,0 +1,32 @@
+"""The hardware microbenchmarks (gather ceiling, streaming-read floor)."""
+
+from __future__ import annotations
+
+import pytest
+
+from tilegen_amd import microbench, runtime
+from tilegen_amd.verify import hiprtc_options
+
+
+def test_probe_kernels_compile():
+    for src in (microbench._GATHER_SRC, microbench._STREAM_SRC):
+        code, _ = runtime.rtc_compile(src, "microbench.hip", hiprtc_options())
+        assert len(code) > 0
+
+
+def test_render_tables():
+    g = [{"kernel": "mb_gather", "lanes_or_uniform": 64, "us": 10.0, "gathers_per_s": 2e11,
+          "gather_instr_per_s": 3e9}]
+    s = [{"mb": 27, "bytes": 27 << 20, "us": 5.0, "gb_per_s": 5600.0, "workgroups": 4096,
+          "copies": 47}]
+    md = microbench.render(g, s, "MI355X gfx950")
+    assert "| mb_gather | 64 | 10.00 | 200.0 | 3.00 |" in md
+    assert "| 27 | 5.00 | 5600 | 4096 |" in md
+
+
+@pytest.mark.gpu
+def test_probes_run(hip_ready):
+    g = microbench.gather_probe(workgroups=512, iters=3)
+    assert len(g) == 8 and all(r["us"] > 0 and r["gathers_per_s"] > 0 for r in g)
+    s = microbench.stream_probe(sizes_mb=(8,), rotate_mb=32, iters=5)
+    assert s[0]["copies"] == 4 and 0 < s[0]["gb_per_s"] < 20000

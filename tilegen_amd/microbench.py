@@ -1,0 +1,223 @@
+"""Hardware microbenchmarks behind the roofline analysis of the SpMV path.
+
+Two probes, each a small kernel compiled with hipRTC and timed with
+dispatch-attached events (``tg_time_launches``); neither is on the product path.
+
+gather
+    Random 8-byte loads from an 800 KB array (the size of c1's ``x``, which
+    stays resident in each XCD's L2), 8 per lane, indices streamed from HBM.
+    Run with 64, 32, 16 and 8 active lanes per wave: if the rate in gathers/s
+    stays flat as lanes drop, the limit is per gathered line, not per load
+    instruction.  A second kernel routes the gathers of the first S lanes of
+    each wave through uniform (scalar-cache) loads instead, to see whether
+    that path adds capacity.
+stream
+    A plain 128-bit read-and-sum over cold (rotated) copies of 8, 27, 128 and
+    512 MB: the practical HBM read rate at the BASELINE sizes, including one
+    launch's ramp-up and first-byte latency.
+
+``python -m tilegen_amd.microbench --out results`` writes ``microbench.json``
+and ``microbench.md``.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+from typing import Dict, List
+
+import numpy as np
+
+from . import runtime as rt
+from .verify import hiprtc_options
+
+__all__ = ["gather_probe", "stream_probe", "main"]
+
+_GATHER_SRC = r'''
+typedef long long i64;
+// 8 gathers per lane from x; lanes at or past `active` in each wave skip theirs
+extern "C" __global__ __launch_bounds__(256)
+void mb_gather(const i64* __restrict__ idx, const double* __restrict__ x, double* __restrict__ out,
+               int active) {
+  const i64 t = (i64)blockIdx.x * 256 + threadIdx.x;
+  double acc = 0.0;
+  if ((int)(threadIdx.x & 63) < active) {
+    i64 c[8];
+    #pragma unroll
+    for (int u = 0; u < 8; ++u) c[u] = idx[t * 8 + u];
+    #pragma unroll
+    for (int u = 0; u < 8; ++u) acc += x[c[u]];
+  }
+  out[t] = acc;
+}
+// the first S lanes' gathers go through wave-uniform loads, one lane at a time
+extern "C" __global__ __launch_bounds__(256)
+void mb_gather_uniform(const i64* __restrict__ idx, const double* __restrict__ x,
+                       double* __restrict__ out, int S) {
+  const i64 t = (i64)blockIdx.x * 256 + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  i64 c[8];
+  #pragma unroll
+  for (int u = 0; u < 8; ++u) c[u] = idx[t * 8 + u];
+  double acc = 0.0;
+  if (lane >= S) {
+    #pragma unroll
+    for (int u = 0; u < 8; ++u) acc += x[c[u]];
+  }
+  for (int l = 0; l < S; ++l) {
+    #pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int lo = __builtin_amdgcn_readlane((int)c[u], l);
+      const int hi = __builtin_amdgcn_readlane((int)(c[u] >> 32), l);
+      const double v = x[((i64)hi << 32) | (unsigned)lo];
+      acc += lane == l ? v : 0.0;
+    }
+  }
+  out[t] = acc;
+}
+'''
+
+_STREAM_SRC = r'''
+typedef double f64x2 __attribute__((ext_vector_type(2)));
+// each workgroup sums its contiguous share of the array with 128-bit loads;
+// the sum is stored only if it equals a sentinel, so the loads cannot be elided
+extern "C" __global__ __launch_bounds__(256)
+void mb_stream(const f64x2* __restrict__ a, double* __restrict__ out, long long n2,
+               long long per_block) {
+  const long long lo = (long long)blockIdx.x * per_block;
+  long long hi = lo + per_block;
+  if (hi > n2) hi = n2;
+  double s = 0.0;
+  for (long long i = lo + threadIdx.x; i < hi; i += 1024) {
+    f64x2 v[4];
+    #pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const long long k = i + u * 256;
+      v[u] = k < hi ? __builtin_nontemporal_load(a + k) : (f64x2){0.0, 0.0};
+    }
+    #pragma unroll
+    for (int u = 0; u < 4; ++u) s += v[u].x + v[u].y;
+  }
+  if (s == 12345.678) out[blockIdx.x] = s;
+}
+'''
+
+
+def _load(src: str, names: List[str]) -> Dict[str, int]:
+    code, _ = rt.rtc_compile(src, "microbench.hip", hiprtc_options())
+    blob = ctypes.create_string_buffer(code, len(code))
+    mod = ctypes.c_void_p()
+    rt.check(rt.lib().tg_module_load(blob, len(code), ctypes.byref(mod)), "module load")
+    _load.keep.append(blob)
+    out = {}
+    for n in names:
+        f = ctypes.c_void_p()
+        rt.check(rt.lib().tg_module_function(mod, n.encode(), ctypes.byref(f)), n)
+        out[n] = f.value
+    return out
+
+
+_load.keep = []
+
+
+def gather_probe(n: int = 100_000, workgroups: int = 4000, iters: int = 30) -> List[dict]:
+    fns = _load(_GATHER_SRC, ["mb_gather", "mb_gather_uniform"])
+    threads = 256 * workgroups
+    rng = np.random.default_rng(0)
+    idx = rng.integers(0, n, threads * 8, dtype=np.int64)
+    if idx.min() < 0 or idx.max() >= n:  # every gather stays inside x
+        raise AssertionError("index out of range")
+    bi, bx = rt.DeviceBuffer(idx), rt.DeviceBuffer(rng.uniform(-1, 1, n))
+    bo = rt.DeviceBuffer(np.zeros(threads))
+    waves = threads // 64
+    rows = []
+    try:
+        for name, arg in [("mb_gather", 64), ("mb_gather", 32), ("mb_gather", 16),
+                          ("mb_gather", 8), ("mb_gather_uniform", 0), ("mb_gather_uniform", 4),
+                          ("mb_gather_uniform", 8), ("mb_gather_uniform", 16)]:
+            kms, _ = rt.time_launches(fns[name], workgroups, 256, 0, [[bi, bx, bo, arg]], 5,
+                                      iters)
+            sec = float(np.median(kms)) * 1e-3
+            gathers = waves * 8 * (arg if name == "mb_gather" else 64)
+            rows.append({"kernel": name, "lanes_or_uniform": arg, "us": sec * 1e6,
+                         "gathers_per_s": gathers / sec, "gather_instr_per_s": waves * 8 / sec})
+    finally:
+        for b in (bi, bx, bo):
+            b.free()
+    return rows
+
+
+def stream_probe(sizes_mb=(8, 27, 128, 512), rotate_mb: int = 1280, iters: int = 100
+                 ) -> List[dict]:
+    fn = _load(_STREAM_SRC, ["mb_stream"])["mb_stream"]
+    out = rt.DeviceBuffer(np.zeros(1 << 16))
+    rows = []
+    try:
+        for mb in sizes_mb:
+            n = (mb << 20) // 8
+            copies = max(2, rotate_mb // mb)
+            bufs = [rt.DeviceBuffer(np.random.default_rng(c).standard_normal(n))
+                    for c in range(copies)]
+            try:
+                best = None
+                for blocks in (2048, 4096, 8192, 16384):
+                    per = -(-(n // 2) // blocks)
+                    kms, _ = rt.time_launches(fn, blocks, 256, 0,
+                                              [[b, out, n // 2, per] for b in bufs], 10, iters)
+                    sec = float(np.median(kms)) * 1e-3
+                    if best is None or sec < best[0]:
+                        best = (sec, blocks)
+                rows.append({"mb": mb, "bytes": n * 8, "us": best[0] * 1e6,
+                             "gb_per_s": n * 8 / best[0] / 1e9, "workgroups": best[1],
+                             "copies": copies})
+            finally:
+                for b in bufs:
+                    b.free()
+    finally:
+        out.free()
+    return rows
+
+
+def render(gather: List[dict], stream: List[dict], device: str) -> str:
+    md = ["# Microbenchmarks (%s)" % device, "",
+          "Written by `python -m tilegen_amd.microbench`; kernel times are medians of "
+          "dispatch-attached events.", "",
+          "## Random 8-byte gathers from an 800 KB (L2-resident) array", "",
+          "| kernel | active lanes / lanes routed through uniform loads | µs | G gathers/s | "
+          "G gather instructions/s |", "|---|---:|---:|---:|---:|"]
+    for r in gather:
+        md.append("| %s | %d | %.2f | %.1f | %.2f |" % (
+            r["kernel"], r["lanes_or_uniform"], r["us"], r["gathers_per_s"] / 1e9,
+            r["gather_instr_per_s"] / 1e9))
+    md += ["", "## Streaming 128-bit reads over cold copies", "",
+           "| MB | µs | GB/s | workgroups |", "|---:|---:|---:|---:|"]
+    for r in stream:
+        md.append("| %d | %.2f | %.0f | %d |" % (r["mb"], r["us"], r["gb_per_s"],
+                                                 r["workgroups"]))
+    return "\n".join(md) + "\n"
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description="Gather and streaming-read microbenchmarks.")
+    ap.add_argument("--out", default="results")
+    a = ap.parse_args(argv)
+    if rt.device_count() < 1:
+        print("microbench: no HIP device visible", file=sys.stderr)
+        return 2
+    dev = rt.device_info(0)
+    g = gather_probe()
+    s = stream_probe()
+    os.makedirs(a.out, exist_ok=True)
+    with open(os.path.join(a.out, "microbench.json"), "w") as fh:
+        json.dump({"device": dev, "gather": g, "stream": s}, fh, indent=1)
+    with open(os.path.join(a.out, "microbench.md"), "w") as fh:
+        fh.write(render(g, s, "%s %s" % (dev["name"], dev["arch"])))
+    print(render(g, s, dev["arch"]))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
