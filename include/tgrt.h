@@ -58,9 +58,14 @@ int tg_module_load(const void* code, size_t code_size, tg_module* module);
 int tg_module_unload(tg_module module);
 int tg_module_function(tg_module module, const char* name, tg_function* fn);
 /* Function `name` of an embedded code object on the current device. Loaded
- * once per (code pointer, device) and kept for the life of the process. */
+ * once per (code pointer, device) and kept until tg_code_release. */
 int tg_code_function(const void* code, size_t code_size, const char* name,
                      tg_function* fn);
+/* Forgets the cached modules of an embedded code object on every device, so
+ * that another object later placed at the same address is loaded afresh.
+ * Generated launcher libraries call it as they are unloaded.  The modules are
+ * not unloaded (this may run during process exit), so this makes no HIP call. */
+int tg_code_release(const void* code, size_t code_size);
 /* Registers, static LDS bytes, scratch bytes per lane, max lanes per workgroup. */
 int tg_function_attrs(tg_function fn, int* num_regs, int* lds_bytes, int* scratch_bytes,
                       int* max_threads);

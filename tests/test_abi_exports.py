@@ -8,6 +8,7 @@ import ctypes
 import os
 import re
 import subprocess
+import sys
 
 import pytest
 
@@ -62,6 +63,25 @@ def test_variant_library_exports_launch_abi(kernel, tmp_path):
     assert lib.tgv_geometry(1000, 1000, 64, 5000, ctypes.byref(g), ctypes.byref(b),
                             ctypes.byref(l)) == 0
     assert b.value == 256 and g.value * gen.geometry.rows_per_block >= 1000
+
+
+def test_variant_unload_releases_its_cached_module(tmp_path):
+    """Unloading a variant library runs its destructor, which drops the
+    runtime's module-cache entry for the library's embedded code object (so a
+    later library mapped at the same address is not served the old kernel),
+    and a process that exits with variants still loaded exits cleanly."""
+    import _ctypes
+    gen = generate(standard_kernels()["spmv"], Config(), "hip", outdir=str(tmp_path))
+    so, _ = compile_generated(gen, "hip", str(tmp_path))
+    L = runtime.lib()
+    assert L.tg_code_release(None, 0) == 0  # nothing cached: no-op
+    lib = ctypes.CDLL(so)
+    _ctypes.dlclose(lib._handle)
+    code = ("import ctypes, sys; sys.path.insert(0, %r); from tilegen_amd import runtime; "
+            "runtime.lib(); ctypes.CDLL(%r); print('ok')" % (ROOT, so))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", r.stderr
 
 
 def test_header_signatures_match_generated_launchers():

@@ -1447,6 +1447,12 @@ def emit_hip_host(kernel: Kernel, config: Config) -> str:
 
 static const unsigned char tg_code[{CODE_SIZE}] = {{CODE_OBJECT}};
 
+/* the runtime caches the loaded module by tg_code's address: drop that entry
+   when this library is unloaded, before another can be mapped there */
+__attribute__((destructor)) static void tgv_unload(void) {
+  tg_code_release(tg_code, sizeof(tg_code));
+}
+
 void* tgv_function(void) {
   tg_function fn = 0;
   if (tg_code_function(tg_code, sizeof(tg_code), "%(sym)s", &fn) != 0) return 0;

@@ -67,9 +67,19 @@ struct CodeKey {
     return std::tie(code, size, device) < std::tie(o.code, o.size, o.device);
   }
 };
-std::mutex g_cache_mu;
-std::map<CodeKey, hipModule_t> g_modules;
-std::map<std::tuple<hipModule_t, std::string>, hipFunction_t> g_functions;
+struct CodeCache {
+  std::mutex mu;
+  std::map<CodeKey, hipModule_t> modules;
+  std::map<std::tuple<hipModule_t, std::string>, hipFunction_t> functions;
+};
+
+// Never destroyed: launcher libraries call tg_code_release from their own ELF
+// destructors, which at process exit can run after this library's static
+// objects would have been torn down.
+CodeCache& code_cache() {
+  static CodeCache* c = new CodeCache;
+  return *c;
+}
 
 bool valid_geometry(int64_t grid, int32_t block) {
   if (grid <= 0 || block <= 0 || block > 1024) return false;
@@ -218,19 +228,20 @@ int tg_code_function(const void* code, size_t code_size, const char* name,
   if (!code || !code_size || !name || !fn) return fail(-1, "tg_code_function: null argument");
   int device = 0;
   TG_HIP(hipGetDevice(&device), "hipGetDevice");
-  std::lock_guard<std::mutex> lock(g_cache_mu);
+  CodeCache& c = code_cache();
+  std::lock_guard<std::mutex> lock(c.mu);
   CodeKey key{code, code_size, device};
-  auto it = g_modules.find(key);
+  auto it = c.modules.find(key);
   hipModule_t m;
-  if (it == g_modules.end()) {
+  if (it == c.modules.end()) {
     TG_HIP(hipModuleLoadData(&m, code), "hipModuleLoadData");
-    g_modules.emplace(key, m);
+    c.modules.emplace(key, m);
   } else {
     m = it->second;
   }
   auto fkey = std::make_tuple(m, std::string(name));
-  auto fit = g_functions.find(fkey);
-  if (fit != g_functions.end()) {
+  auto fit = c.functions.find(fkey);
+  if (fit != c.functions.end()) {
     *fn = fit->second;
     return 0;
   }
@@ -238,8 +249,24 @@ int tg_code_function(const void* code, size_t code_size, const char* name,
   hipError_t e = hipModuleGetFunction(&f, m, name);
   if (e != hipSuccess)
     return fail(static_cast<int>(e), "hipModuleGetFunction(%s): %s", name, hipGetErrorString(e));
-  g_functions.emplace(fkey, f);
+  c.functions.emplace(fkey, f);
   *fn = f;
+  return 0;
+}
+
+int tg_code_release(const void* code, size_t code_size) {
+  CodeCache& c = code_cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  for (auto it = c.modules.begin(); it != c.modules.end();) {
+    if (it->first.code == code && it->first.size == code_size) {
+      const hipModule_t m = it->second;
+      for (auto f = c.functions.begin(); f != c.functions.end();)
+        f = std::get<0>(f->first) == m ? c.functions.erase(f) : std::next(f);
+      it = c.modules.erase(it);
+    } else {
+      ++it;
+    }
+  }
   return 0;
 }
 

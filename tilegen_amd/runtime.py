@@ -78,6 +78,7 @@ def _declare(L) -> None:
         "tg_module_function": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(_vp)]),
         "tg_code_function": (ctypes.c_int, [_vp, ctypes.c_size_t, ctypes.c_char_p,
                                             ctypes.POINTER(_vp)]),
+        "tg_code_release": (ctypes.c_int, [_vp, ctypes.c_size_t]),
         "tg_function_attrs": (ctypes.c_int, [_vp, _c_int_p, _c_int_p, _c_int_p, _c_int_p]),
         "tg_launch": (ctypes.c_int, [_vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                      _c_u64_p, ctypes.c_int, _vp, ctypes.c_int]),
