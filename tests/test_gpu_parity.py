@@ -17,7 +17,8 @@ from tests.util import csr, mixed_257, ragged, rel_2, rel_inf
 from tilegen_amd.codegen import Config
 from tilegen_amd.matrices import make_baseline
 from tilegen_amd.schedules import TEST_KERNELS, TEST_SCHEDULES, schedule_id
-from tilegen_amd.variant import Variant
+from tilegen_amd import runtime as rt
+from tilegen_amd.variant import Variant, operand_order
 from tilegen_amd.verify import _inputs_for, _reference, verify
 
 pytestmark = pytest.mark.gpu
@@ -232,3 +233,88 @@ def test_sddmm_wide_k_skewed_rows(cfg, hip_ready):
     for label, A in cases.items():
         for K in (130, 257):
             _check("sddmm", cfg, A, K=K, label="%s K=%d" % (label, K))
+
+
+class _View(rt.DeviceBuffer):
+    """A device pointer into another buffer (a caller's sub-buffer); the base
+    buffer owns the memory."""
+
+    def __init__(self, base: rt.DeviceBuffer, offset: int, nbytes: int):
+        self.array, self.nbytes, self.ptr, self._base = None, nbytes, base.ptr + offset, base
+
+    def free(self) -> None:
+        self.ptr = 0
+
+
+GUARD = -7.25e300
+
+
+def _guarded(arr: np.ndarray):
+    """``arr`` placed 8 bytes into an allocation (so only 8-byte aligned), with
+    one guard element on each side; returns (base, view)."""
+    a = np.ascontiguousarray(arr).ravel()
+    dt = a.dtype
+    guard = np.array([GUARD], dtype=np.float64).view(dt) if dt.itemsize == 8 else None
+    base = rt.DeviceBuffer(np.concatenate([guard, a, guard]))
+    return base, _View(base, 8, a.nbytes)
+
+
+OFFSET_CASES = [
+    ("spmv", Config(tile_size=16, threads_per_row=8, unroll=2, block_size=128)),
+    ("spmv", Config(tile_size=64, threads_per_row=4, unroll=4, block_size=256)),
+    ("spmv", Config(tile_size=4, threads_per_row=64, unroll=2, block_size=256)),
+    ("fused_spmv_axpy", Config(tile_size=128, threads_per_row=4, unroll=2, block_size=256)),
+    ("spmm", Config(tile_size=16, threads_per_row=16, unroll=2, vector_width=2, block_size=64)),
+    ("spmm", Config(tile_size=4, threads_per_row=64, unroll=2, vector_width=2, block_size=256)),
+    ("sddmm", Config(tile_size=16, threads_per_row=8, unroll=4, vector_width=2, block_size=128)),
+    ("sddmm", Config(tile_size=8, threads_per_row=16, unroll=2, vector_width=2, block_size=128)),
+    ("axpy", Config(tile_size=64, threads_per_row=1, unroll=4, vector_width=2, block_size=256)),
+]
+
+
+@pytest.mark.parametrize("kernel,cfg", OFFSET_CASES,
+                         ids=["%s-%s" % (k, schedule_id(c)) for k, c in OFFSET_CASES])
+def test_operands_at_8_byte_offsets(kernel, cfg, hip_ready):
+    """Every array argument (indptr, indices, data, dense operands, output)
+    starts 8 bytes into its allocation, as a caller's sub-buffer can: the
+    128-bit paths must notice and fall back, results must stay at the bar, and
+    the guard elements either side of every array must be untouched."""
+    A = ragged(26, 700, 900, 40, empty_every=6, long_rows=[(3, 800), (699, 500)])
+    K = 64 if kernel in ("spmm", "sddmm") else 0
+    ops = _operands(kernel, A, max(K, 1))
+    M, N = A.shape
+    host = {}
+    if kernel != "axpy":
+        host.update(indptr=A.indptr.astype(np.int64), indices=A.indices.astype(np.int64),
+                    data=A.data.astype(np.float64))
+    dense, scal, _ = operand_order(kernel)
+    for d in dense:
+        host[d] = np.asarray(ops[d], dtype=np.float64)
+    out_name, out_shape = {"spmv": ("y", (M,)), "fused_spmv_axpy": ("z", (M,)),
+                           "axpy": ("z", (M,)), "spmm": ("C", (M, K)),
+                           "sddmm": ("C", (A.nnz,))}[kernel]
+    host[out_name] = np.zeros(out_shape)
+    if kernel == "axpy":
+        host["x"], host["w"] = host["x"][:M], host["w"][:M]
+    pairs = {k: _guarded(v) for k, v in host.items()}
+    try:
+        v = Variant(kernel, cfg)
+        vals = v.abi_values(A, {k: p[1] for k, p in pairs.items()},
+                            {s: float(ops[s]) for s in scal}, M, N, K, A.nnz)
+        v.device_call(vals)
+        for k, (base, _view) in pairs.items():
+            full = base.to_host()
+            assert full[:1].view(np.float64)[0] == GUARD, (k, "guard before")
+            assert full[-1:].view(np.float64)[0] == GUARD, (k, "guard after")
+            if k != out_name:
+                assert full[1:-1].tobytes() == host[k].tobytes(), (k, "input modified")
+        out = pairs[out_name][0].to_host()[1:-1].reshape(out_shape)
+    finally:
+        for base, view in pairs.values():
+            view.free()
+            base.free()
+    if kernel == "axpy":
+        want = oracle.axpy(host["x"], host["w"], ops["alpha"], ops["beta"])
+    else:
+        want = oracle.compute(kernel, A, {k: host.get(k, ops[k]) for k in ops})
+    assert rel_inf(out, want) <= TOL and rel_2(out, want) <= TOL

@@ -16,7 +16,8 @@ backend "hip"
         ThreadsPerRow(k) lanes per row with a segmented DPP butterfly over k
         lanes of a 64-lane wave; Unroll(u) = each lane owns u consecutive
         nonzeros per step, loaded as 128-bit pairs from a 16-byte aligned base
-        (row starts are rounded down, the extra lanes masked); Tile(T) = a
+        (row starts are rounded down, the extra lanes masked; bases that are
+        only 8-byte aligned take per-element loads); Tile(T) = a
         workgroup owns T rows whose row pointers are staged once in LDS and
         whose first step is issued for every row before any gather, so each
         wave keeps several rows of loads in flight.
@@ -742,6 +743,11 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w("const tg_i64 row0 = (tg_i64)blockIdx.x * %d;" % TR)
     w("const int lane = threadIdx.x %% %d;" % TPR)
     w("const int slot = threadIdx.x / %d;" % TPR)
+    if U % 2 == 0:
+        w("// 128-bit (index, value) pair loads need 16-byte aligned bases; a caller's")
+        w("// sub-buffer may be only 8-byte aligned, which takes the per-element loads")
+        w("const bool pair_ok = ((((unsigned long long)indices) | "
+          "((unsigned long long)data)) & 15) == 0;")
     if low.tiled:
         w("// row pointers of this tile, staged once in LDS")
         w("__shared__ tg_i64 s_ptr[%d];" % (TR + 1))
@@ -785,7 +791,7 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         """Load U consecutive nonzeros at q (masked to [lo, hi)), gather, FMA."""
         w("tg_i64 ci[%d]; double cv[%d];" % (U, U))
         if U % 2 == 0:
-            w.open("if (%s + %d <= nnz)" % (q, U))
+            w.open("if (pair_ok && %s + %d <= nnz)" % (q, U))
             for u in range(0, U, 2):
                 w("{ const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + %s + %d));"
                   " ci[%d] = a.x; ci[%d] = a.y; }" % (q, u, u, u + 1))
