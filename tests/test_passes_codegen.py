@@ -160,16 +160,27 @@ def test_hip_no_reduction_when_one_lane_per_row():
     src = _hip("spmv", Config(tile_size=128, threads_per_row=1, unroll=2, block_size=128))
     body = _code(src).split("tg_uniform(tg_i64 v)")[1]
     assert "acc[r] = tg_segsum" not in body
-    # only the workgroup path for long rows reduces across lanes
-    assert body.count("tg_segsum<") == 1 and "cacc = tg_segsum<64>(cacc);" in body
+    # only the wave path for medium rows and the workgroup path for long rows
+    # reduce across lanes
+    assert body.count("tg_segsum<") == 2
+    assert "macc = tg_segsum<64>(macc);" in body and "cacc = tg_segsum<64>(cacc);" in body
 
 
-def test_hip_long_rows_go_to_the_workgroup_only_when_tiled():
+def test_hip_long_rows_leave_the_lane_group_only_when_tiled():
+    # narrow lane groups: rows over 2 steps go to a wave, over 4 wave steps to
+    # the workgroup
     cfg = Config(tile_size=64, threads_per_row=4, unroll=2, block_size=256)
     tiled = _hip("spmv", cfg)
-    assert "coop[r] = re[r] - rs[r] > 64;" in tiled  # 8 steps of 4 lanes x 2 nonzeros
-    assert "s_long[atomicAdd(&s_nlong, 1)] = lr;" in tiled
-    assert "s_long[" not in _hip("spmv", cfg, skip=("tiling",))
+    assert "coop[r] = re[r] - rs[r] > 16;" in tiled  # 2 steps of 4 lanes x 2 nonzeros
+    assert "if (re[r] - rs[r] > 512) s_long[atomicAdd(&s_nlong, 1)] = lr;" in tiled
+    assert "else s_med[atomicAdd(&s_nmed, 1)] = lr;" in tiled
+    assert "for (int k = wv; k < n_med; k += 4)" in tiled  # medium rows spread over the waves
+    untiled = _hip("spmv", cfg, skip=("tiling",))
+    assert "s_long[" not in untiled and "s_med[" not in untiled
+    # lane groups of 32 or more go straight to the workgroup after 8 steps
+    wide = _hip("spmv", Config(tile_size=32, threads_per_row=32, unroll=2, block_size=1024))
+    assert "coop[r] = re[r] - rs[r] > 512;" in wide and "s_med[" not in wide
+    assert "if (lane == 0) s_long[atomicAdd(&s_nlong, 1)] = lr;" in wide
 
 
 def test_skipping_tiling_changes_hip_and_cpu_code():

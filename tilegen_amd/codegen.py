@@ -724,7 +724,10 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     longer than LONG nonzeros (8 lane-group steps) is not walked by its lane
     group; the group appends it to an LDS list, and after the lane-group phase
     the whole workgroup takes each listed row in turn with coalesced loads and
-    a wave + LDS reduction.
+    a wave + LDS reduction.  Lane groups of 16 lanes or fewer add a middle
+    tier: rows over 2 group steps and up to 4 wave steps go to a second list
+    whose rows the waves share out, one row per wave at a time, reduced within
+    the wave (no barrier); only rows past that go to the workgroup.
     """
     B, TPR = geo.block, max(1, low.threads_per_row)
     U = max(1, low.unroll)
@@ -736,6 +739,12 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     LONG = 8 * STEP    # longer rows leave their lane group
     WAVES = B // WAVE
     coop = low.tiled
+    # narrow lane groups hand rows over 2 steps to a whole wave, and rows over
+    # 4 wave steps to the workgroup
+    wave_tier = coop and TPR <= 16
+    if wave_tier:
+        LONG = 2 * STEP
+        WLONG = 4 * WAVE * U
     row = plan.row_idx.name
     col = plan.col_idx.name
 
@@ -753,8 +762,11 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("__shared__ tg_i64 s_ptr[%d];" % (TR + 1))
         w("__shared__ int s_long[%d];   // rows left to the whole workgroup" % TR)
         w("__shared__ int s_nlong;")
+        if wave_tier:
+            w("__shared__ int s_med[%d];    // rows left to one wave each" % TR)
+            w("__shared__ int s_nmed;")
         w("__shared__ double s_red[%d];" % WAVES)
-        w("if (threadIdx.x == 0) s_nlong = 0;")
+        w("if (threadIdx.x == 0) { s_nlong = 0;%s }" % (" s_nmed = 0;" if wave_tier else ""))
         w.open("for (int t = threadIdx.x; t <= %d; t += %d)" % (TR, B))
         w("const tg_i64 r = row0 + t;")
         w("s_ptr[t] = indptr[r < row_end ? r : row_end];")
@@ -779,7 +791,13 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     if coop:
         w("coop[r] = re[r] - rs[r] > %d;" % LONG)
         w.open("if (coop[r])")
-        w("if (lane == 0) s_long[atomicAdd(&s_nlong, 1)] = lr;")
+        if wave_tier:
+            w.open("if (lane == 0)")
+            w("if (re[r] - rs[r] > %d) s_long[atomicAdd(&s_nlong, 1)] = lr;" % WLONG)
+            w("else s_med[atomicAdd(&s_nmed, 1)] = lr;")
+            w.close()
+        else:
+            w("if (lane == 0) s_long[atomicAdd(&s_nlong, 1)] = lr;")
         w("re[r] = rs[r];  // the lane group skips it")
         w.close()
     w("acc[r] = 0.0;")
@@ -857,8 +875,31 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w.close()
     if not coop:
         return
-    w("// long rows: the whole workgroup, one row at a time")
     w("__syncthreads();")
+    if wave_tier:
+        w("// medium rows: one wave each, no barriers")
+        w("const int n_med = s_nmed;")
+        w("const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / %d);" % WAVE)
+        w("const int wl = threadIdx.x %% %d;" % WAVE)
+        w("#pragma unroll 1")
+        w.open("for (int k = wv; k < n_med; k += %d)" % WAVES)
+        w("const int lr = s_med[k];")
+        w("const tg_i64 row = row0 + lr;")
+        w("const tg_i64 mrs = s_ptr[lr], mre = s_ptr[lr + 1];")
+        w("double macc = 0.0;")
+        w("#pragma unroll 1")
+        w.open("for (tg_i64 q = (mrs & ~(tg_i64)%d) + (tg_i64)wl * %d; q < mre; q += %d)"
+               % (ALIGN - 1, U, WAVE * U))
+        step("q", "mrs", "mre", "macc")
+        w.close()
+        w("macc = tg_segsum<%d>(macc);" % WAVE)
+        w.open("if (wl == 0)")
+        env = _Env({row: "row"}, acc="macc")
+        w("__builtin_nontemporal_store(%s, %s + %s);" % (
+            _cexpr(plan.final_expr, env), out_name, _offset(plan.out_tensor, plan.out.indices, env)))
+        w.close()
+        w.close()
+    w("// long rows: the whole workgroup, one row at a time")
     w("const int n_long = s_nlong;")
     w("#pragma unroll 1")
     w.open("for (int k = 0; k < n_long; ++k)")
