@@ -73,14 +73,16 @@ def test_matches_oracle_k64(kernel, cfg, hip_ready):
 
 
 @pytest.mark.parametrize("kernel", ["spmm", "sddmm"])
-@pytest.mark.parametrize("K", [1, 7, 63, 130])
+@pytest.mark.parametrize("K", [1, 7, 63, 130, 1024, 2049])
 def test_odd_and_wide_K(kernel, K, hip_ready):
     """K not a multiple of the vector width (scalar fallback) and K wider than
-    one pass of the lanes."""
+    one pass of the lanes, up to many passes (1024, and 2049 odd)."""
     for cfg in (Config(tile_size=8, threads_per_row=32, unroll=4, vector_width=2,
                        block_size=256),
                 Config(tile_size=4, threads_per_row=4, unroll=2, vector_width=2,
-                       block_size=256)):
+                       block_size=256),
+                Config(tile_size=16, threads_per_row=8, unroll=4, vector_width=2,
+                       block_size=128)):
         _check(kernel, cfg, mixed_257(), K=K, label="K=%d" % K)
 
 
