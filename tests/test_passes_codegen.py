@@ -171,7 +171,10 @@ def test_hip_long_rows_leave_the_lane_group_only_when_tiled():
     # the workgroup
     cfg = Config(tile_size=64, threads_per_row=4, unroll=2, block_size=256)
     tiled = _hip("spmv", cfg)
-    assert "coop[r] = re[r] - rs[r] > 16;" in tiled  # 2 steps of 4 lanes x 2 nonzeros
+    # over 2 steps of 4 lanes x 2 nonzeros and over twice the tile's average row,
+    # or over 8 steps outright
+    assert "coop[r] = len > 16 && (len * t_rows > 2 * t_nnz || len > 64);" in tiled
+    assert "const tg_i64 t_nnz = s_ptr[64] - s_ptr[0];" in tiled
     assert "if (re[r] - rs[r] > 512) s_long[atomicAdd(&s_nlong, 1)] = lr;" in tiled
     assert "else s_med[atomicAdd(&s_nmed, 1)] = lr;" in tiled
     assert "for (int k = wv; k < n_med; k += 4)" in tiled  # medium rows spread over the waves

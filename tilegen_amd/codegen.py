@@ -739,11 +739,12 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     LONG = 8 * STEP    # longer rows leave their lane group
     WAVES = B // WAVE
     coop = low.tiled
-    # narrow lane groups hand rows over 2 steps to a whole wave, and rows over
-    # 4 wave steps to the workgroup
+    # narrow lane groups also hand a row over 2 steps that is more than twice
+    # its tile's average to a whole wave (rows over 8 steps always leave), and
+    # rows over 4 wave steps go to the workgroup
     wave_tier = coop and TPR <= 16
     if wave_tier:
-        LONG = 2 * STEP
+        MED = 2 * STEP
         WLONG = 4 * WAVE * U
     row = plan.row_idx.name
     col = plan.col_idx.name
@@ -772,6 +773,10 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("s_ptr[t] = indptr[r < row_end ? r : row_end];")
         w.close()
         w("__syncthreads();")
+        if wave_tier:
+            w("// rows and nonzeros of this tile (s_ptr[%d] is clamped to the last row)" % TR)
+            w("const tg_i64 t_rows = row_end - row0 < %d ? row_end - row0 : %d;" % (TR, TR))
+            w("const tg_i64 t_nnz = s_ptr[%d] - s_ptr[0];" % TR)
     w("tg_i64 rs[%d], re[%d];" % (R, R))
     w("double acc[%d];" % R)
     if coop:
@@ -789,7 +794,11 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("rs[r] = live ? indptr[ri] : 0;")
         w("re[r] = live ? indptr[ri + 1] : 0;")
     if coop:
-        w("coop[r] = re[r] - rs[r] > %d;" % LONG)
+        if wave_tier:
+            w("const tg_i64 len = re[r] - rs[r];")
+            w("coop[r] = len > %d && (len * t_rows > 2 * t_nnz || len > %d);" % (MED, LONG))
+        else:
+            w("coop[r] = re[r] - rs[r] > %d;" % LONG)
         w.open("if (coop[r])")
         if wave_tier:
             w.open("if (lane == 0)")
