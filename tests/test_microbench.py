@@ -30,3 +30,20 @@ def test_probes_run(hip_ready):
     assert len(g) == 8 and all(r["us"] > 0 and r["gathers_per_s"] > 0 for r in g)
     s = microbench.stream_probe(sizes_mb=(8,), rotate_mb=32, iters=5)
     assert s[0]["copies"] == 4 and 0 < s[0]["gb_per_s"] < 20000
+
+
+def test_rowgather_kernel_compiles_and_renders():
+    code, _ = runtime.rtc_compile(microbench._ROWGATHER_SRC, "rg.hip", hiprtc_options())
+    assert len(code) > 0
+    rg = [{"table_mb": 51.2, "cold": True, "copies": 13, "rows_gathered": 1600000,
+           "us": 100.0, "g_rows_per_s": 16.0, "gathered_gb_per_s": 8192.0,
+           "written_gb_per_s": 512.0}]
+    assert "| 51.2 | cold (13 copies) | 100.00 | 16.00 | 8192 | 512 |" in microbench.render(
+        [], [], "x", rg)
+
+
+@pytest.mark.gpu
+def test_rowgather_probe_runs(hip_ready):
+    r = microbench.rowgather_probe(table_rows=(6_250,), n_groups=2_000, per=8, rotate_mb=8,
+                                   iters=3)
+    assert len(r) == 2 and all(x["us"] > 0 for x in r)

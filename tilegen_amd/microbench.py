@@ -1,6 +1,6 @@
-"""Hardware microbenchmarks behind the roofline analysis of the SpMV path.
+"""Hardware microbenchmarks behind the roofline analysis of the CSR kernels.
 
-Two probes, each a small kernel compiled with hipRTC and timed with
+Three probes, each a small kernel compiled with hipRTC and timed with
 dispatch-attached events (``tg_time_launches``); neither is on the product path.
 
 gather
@@ -15,6 +15,11 @@ stream
     A plain 128-bit read-and-sum over cold (rotated) copies of 8, 27, 128 and
     512 MB: the practical HBM read rate at the BASELINE sizes, including one
     launch's ramp-up and first-byte latency.
+rowgather
+    SpMM's B-row access without the A stream: 1.6 M random 512-byte rows
+    gathered from a 51.2 MB table (larger than an XCD's L2, smaller than the
+    Infinity Cache) and from a 3.2 MB one, with one 512-byte row written per
+    16 gathered, cold (table copies rotated) and warm.
 
 ``python -m tilegen_amd.microbench --out results`` writes ``microbench.json``
 and ``microbench.md``.
@@ -34,7 +39,7 @@ import numpy as np
 from . import runtime as rt
 from .verify import hiprtc_options
 
-__all__ = ["gather_probe", "stream_probe", "main"]
+__all__ = ["gather_probe", "stream_probe", "rowgather_probe", "main"]
 
 _GATHER_SRC = r'''
 typedef long long i64;
@@ -77,6 +82,33 @@ void mb_gather_uniform(const i64* __restrict__ idx, const double* __restrict__ x
     }
   }
   out[t] = acc;
+}
+'''
+
+_ROWGATHER_SRC = r'''
+typedef long long i64;
+typedef double f64x2 __attribute__((ext_vector_type(2)));
+// each 32-lane group gathers `per` random 512-byte rows of T (64 doubles, one
+// 128-bit load per lane, 4 rows in flight), sums them and writes its 512-byte
+// result row: SpMM's B-row gathers and C stores without the A stream
+extern "C" __global__ __launch_bounds__(256)
+void mb_rowgather(const i64* __restrict__ idx, const f64x2* __restrict__ T, f64x2* __restrict__ out,
+                  i64 n_groups, int per) {
+  const i64 g = ((i64)blockIdx.x * 256 + threadIdx.x) / 32;
+  const int l = threadIdx.x % 32;
+  if (g >= n_groups) return;
+  f64x2 acc = {0.0, 0.0};
+  for (int r = 0; r < per; r += 4) {
+    i64 j[4];
+    #pragma unroll
+    for (int u = 0; u < 4; ++u) j[u] = idx[g * per + r + u];
+    f64x2 v[4];
+    #pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = T[j[u] * 32 + l];
+    #pragma unroll
+    for (int u = 0; u < 4; ++u) acc += v[u];
+  }
+  __builtin_nontemporal_store(acc, out + g * 32 + l);
 }
 '''
 
@@ -181,7 +213,52 @@ def stream_probe(sizes_mb=(8, 27, 128, 512), rotate_mb: int = 1280, iters: int =
     return rows
 
 
-def render(gather: List[dict], stream: List[dict], device: str) -> str:
+def rowgather_probe(table_rows=(100_000, 6_250), n_groups: int = 100_000, per: int = 16,
+                    rotate_mb: int = 640, iters: int = 50) -> List[dict]:
+    """Random 512-byte row gathers (c4's B-row access: 100000 groups x 16
+    rows from a 100000 x 64 fp64 table), cold (table copies rotated past the
+    256 MB Infinity Cache) and warm (one copy)."""
+    if per % 4:
+        raise ValueError("per must be a multiple of 4")
+    fn = _load(_ROWGATHER_SRC, ["mb_rowgather"])["mb_rowgather"]
+    rng = np.random.default_rng(1)
+    out = rt.DeviceBuffer(nbytes=n_groups * 512)
+    grid = -(-n_groups * 32 // 256)
+    rows = []
+    try:
+        for n in table_rows:
+            idx = rng.integers(0, n, n_groups * per, dtype=np.int64)
+            if idx.min() < 0 or idx.max() >= n:  # every gather stays inside the table
+                raise AssertionError("index out of range")
+            bi = rt.DeviceBuffer(idx)
+            table = rng.uniform(-1, 1, (n, 64))
+            try:
+                for cold in (True, False):
+                    copies = max(2, -(-(rotate_mb << 20) // table.nbytes)) if cold else 1
+                    bufs = [rt.DeviceBuffer(table) for _ in range(copies)]
+                    try:
+                        kms, _ = rt.time_launches(fn, grid, 256, 0,
+                                                  [[bi, b, out, n_groups, per] for b in bufs],
+                                                  10, iters)
+                    finally:
+                        for b in bufs:
+                            b.free()
+                    sec = float(np.median(kms)) * 1e-3
+                    g = n_groups * per
+                    rows.append({"table_mb": table.nbytes / 1e6, "cold": cold, "copies": copies,
+                                 "rows_gathered": g, "us": sec * 1e6,
+                                 "g_rows_per_s": g / sec / 1e9,
+                                 "gathered_gb_per_s": g * 512 / sec / 1e9,
+                                 "written_gb_per_s": n_groups * 512 / sec / 1e9})
+            finally:
+                bi.free()
+    finally:
+        out.free()
+    return rows
+
+
+def render(gather: List[dict], stream: List[dict], device: str,
+           rowgather: List[dict] = ()) -> str:
     md = ["# Microbenchmarks (%s)" % device, "",
           "Written by `python -m tilegen_amd.microbench`; kernel times are medians of "
           "dispatch-attached events.", "",
@@ -197,6 +274,15 @@ def render(gather: List[dict], stream: List[dict], device: str) -> str:
     for r in stream:
         md.append("| %d | %.2f | %.0f | %d |" % (r["mb"], r["us"], r["gb_per_s"],
                                                  r["workgroups"]))
+    if rowgather:
+        md += ["", "## Random 512-byte row gathers (SpMM's B rows: 100000 x 16 gathers, "
+               "one 512-byte row written per 16)", "",
+               "| table MB | inputs | µs | G rows/s | GB/s gathered | GB/s written |",
+               "|---:|---|---:|---:|---:|---:|"]
+        for r in rowgather:
+            md.append("| %.1f | %s | %.2f | %.2f | %.0f | %.0f |" % (
+                r["table_mb"], "cold (%d copies)" % r["copies"] if r["cold"] else "warm",
+                r["us"], r["g_rows_per_s"], r["gathered_gb_per_s"], r["written_gb_per_s"]))
     return "\n".join(md) + "\n"
 
 
@@ -210,12 +296,13 @@ def main(argv=None) -> int:
     dev = rt.device_info(0)
     g = gather_probe()
     s = stream_probe()
+    rg = rowgather_probe()
     os.makedirs(a.out, exist_ok=True)
     with open(os.path.join(a.out, "microbench.json"), "w") as fh:
-        json.dump({"device": dev, "gather": g, "stream": s}, fh, indent=1)
+        json.dump({"device": dev, "gather": g, "stream": s, "rowgather": rg}, fh, indent=1)
     with open(os.path.join(a.out, "microbench.md"), "w") as fh:
-        fh.write(render(g, s, "%s %s" % (dev["name"], dev["arch"])))
-    print(render(g, s, dev["arch"]))
+        fh.write(render(g, s, "%s %s" % (dev["name"], dev["arch"]), rg))
+    print(render(g, s, dev["arch"], rg))
     return 0
 
 
