@@ -320,3 +320,27 @@ def test_operands_at_8_byte_offsets(kernel, cfg, hip_ready):
     else:
         want = oracle.compute(kernel, A, {k: host.get(k, ops[k]) for k in ops})
     assert rel_inf(out, want) <= TOL and rel_2(out, want) <= TOL
+
+
+@pytest.mark.parametrize("kernel", ["spmv", "spmm", "sddmm", "fused_spmv_axpy"])
+def test_matrices_without_nonzeros(kernel, hip_ready):
+    """No nonzeros at all (every row empty) and no rows: SpMV/SpMM outputs are
+    all zero even when the output buffer starts with NaNs (written, not
+    accumulated), SDDMM's output is empty, and verify() passes."""
+    cfgs = (Config(tile_size=16, threads_per_row=8, unroll=2, vector_width=2, block_size=128),
+            Config(tile_size=32, threads_per_row=1, unroll=1, vector_width=1, block_size=128))
+    empty = csr(100, 50, np.zeros(101, dtype=np.int64), [], [])
+    norows = csr(0, 50, np.zeros(1, dtype=np.int64), [], [])
+    for A in (empty, norows):
+        M, N = A.shape
+        ops = _operands(kernel, A, 8)
+        for cfg in cfgs:
+            v = Variant(kernel, cfg)
+            shape = {"spmv": (M,), "fused_spmv_axpy": (M,), "spmm": (M, 8), "sddmm": (0,)}[kernel]
+            dense = {k: ops[k] for k in operand_order(kernel)[0] + operand_order(kernel)[1]}
+            out = v.run(A, out=np.full(shape, np.nan), **dense)
+            assert out.shape == tuple(shape)
+            want = _oracle(kernel, A, ops).reshape(shape)
+            assert np.array_equal(out, want), (kernel, cfg.short(), M)
+            r = verify(kernel, cfg, A, backend="hip", K=8)
+            assert r.ok, r.message
