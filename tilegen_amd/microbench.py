@@ -1,7 +1,7 @@
 """Hardware microbenchmarks behind the roofline analysis of the CSR kernels.
 
-Three probes, each a small kernel compiled with hipRTC and timed with
-dispatch-attached events (``tg_time_launches``); neither is on the product path.
+Four probes, each a small kernel compiled with hipRTC and timed with
+dispatch-attached events (``tg_time_launches``); none is on the product path.
 
 gather
     Random 8-byte loads from an 800 KB array (the size of c1's ``x``, which
@@ -20,6 +20,13 @@ rowgather
     gathered from a 51.2 MB table (larger than an XCD's L2, smaller than the
     Infinity Cache) and from a 3.2 MB one, with one 512-byte row written per
     16 gathered, cold (table copies rotated) and warm.
+flat
+    c1's SpMV accesses without its rows: the c1 matrix's own ``indices`` and
+    ``data`` streamed with one 128-bit load of each per lane, ``x`` gathered at
+    those indices, 8 lanes summing 16 products and one double stored per 16,
+    with no row pointers, LDS or barriers.  Cold (every array rotated) and
+    warm, with the gathers and without them (the stream alone): the floor for
+    the bytes and gathers c1 makes, against which the row logic is measured.
 
 ``python -m tilegen_amd.microbench --out results`` writes ``microbench.json``
 and ``microbench.md``.
@@ -39,7 +46,7 @@ import numpy as np
 from . import runtime as rt
 from .verify import hiprtc_options
 
-__all__ = ["gather_probe", "stream_probe", "rowgather_probe", "main"]
+__all__ = ["gather_probe", "stream_probe", "rowgather_probe", "flat_probe", "main"]
 
 _GATHER_SRC = r'''
 typedef long long i64;
@@ -109,6 +116,32 @@ void mb_rowgather(const i64* __restrict__ idx, const f64x2* __restrict__ T, f64x
     for (int u = 0; u < 4; ++u) acc += v[u];
   }
   __builtin_nontemporal_store(acc, out + g * 32 + l);
+}
+'''
+
+_FLAT_SRC = r'''
+typedef long long i64;
+typedef long long i64x2 __attribute__((ext_vector_type(2)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
+// thread t takes nonzeros 2t and 2t+1 (one 128-bit load of indices and one of
+// values); the 8 threads of group g = t / 8 cover nonzeros 16g .. 16g+15 and
+// store their sum as out[g].  With gather == 0 the index itself stands in for
+// x[index], so the index loads stay live and x is never read.
+extern "C" __global__ __launch_bounds__(256)
+void mb_flat(const i64x2* __restrict__ idx, const f64x2* __restrict__ val,
+             const double* __restrict__ x, double* __restrict__ out, i64 n_groups, int gather) {
+  const i64 t = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  const i64 g = t / 8;
+  double s = 0.0;
+  if (g < n_groups) {
+    const i64x2 c = __builtin_nontemporal_load(idx + t);
+    const f64x2 v = __builtin_nontemporal_load(val + t);
+    s = gather ? v.x * x[c.x] + v.y * x[c.y] : v.x * (double)c.x + v.y * (double)c.y;
+  }
+  s += __shfl_xor(s, 1);
+  s += __shfl_xor(s, 2);
+  s += __shfl_xor(s, 4);
+  if (g < n_groups && (threadIdx.x & 7) == 0) __builtin_nontemporal_store(s, out + g);
 }
 '''
 
@@ -257,23 +290,80 @@ def rowgather_probe(table_rows=(100_000, 6_250), n_groups: int = 100_000, per: i
     return rows
 
 
+def flat_probe(rotate_mb: int = 1280, iters: int = 100, blocks=(128, 256)) -> List[dict]:
+    """c1's indices/data/x accesses with no row structure (see the module
+    docstring), on the BASELINE c1 matrix itself."""
+    from .matrices import baseline_operands, make_baseline
+    fn = _load(_FLAT_SRC, ["mb_flat"])["mb_flat"]
+    A = make_baseline("c1")
+    M, N = A.shape
+    nnz = int(A.nnz)
+    if nnz % 16:
+        raise ValueError("the flat probe needs a multiple of 16 nonzeros, got %d" % nnz)
+    indices = np.ascontiguousarray(A.indices, dtype=np.int64)
+    if indices.min() < 0 or indices.max() >= N:  # every gather stays inside x
+        raise AssertionError("index out of range")
+    data = np.ascontiguousarray(A.data, dtype=np.float64)
+    x = baseline_operands("spmv", M, N, 1)["x"]
+    n_groups = nnz // 16
+    per_copy = indices.nbytes + data.nbytes + x.nbytes
+    want = {1: np.add.reduceat(data * x[indices], np.arange(0, nnz, 16)),
+            0: np.add.reduceat(data * indices.astype(np.float64), np.arange(0, nnz, 16))}
+    out = rt.DeviceBuffer(nbytes=n_groups * 8)
+    rows = []
+    try:
+        for cold in (True, False):
+            copies = max(2, -(-(rotate_mb << 20) // per_copy)) if cold else 1
+            sets = [(rt.DeviceBuffer(indices), rt.DeviceBuffer(data), rt.DeviceBuffer(x))
+                    for _ in range(copies)]
+            try:
+                for gather in (1, 0):
+                    for block in blocks:
+                        grid = -(-n_groups * 8 // block)
+                        kms, _ = rt.time_launches(
+                            fn, grid, block, 0,
+                            [[bi, bv, bx, out, n_groups, gather] for bi, bv, bx in sets],
+                            10, iters)
+                        got = out.to_host(np.empty(n_groups))
+                        err = float(np.abs(got - want[gather]).max()
+                                    / max(np.abs(want[gather]).max(), 1e-300))
+                        if not err <= 1e-12:
+                            raise AssertionError("mb_flat result off by %.3e" % err)
+                        sec = float(np.median(kms)) * 1e-3
+                        streamed = indices.nbytes + data.nbytes + n_groups * 8
+                        rows.append({"cold": cold, "copies": copies, "gather": bool(gather),
+                                     "block": block, "nnz": nnz, "us": sec * 1e6,
+                                     "streamed_bytes": streamed,
+                                     "streamed_gb_per_s": streamed / sec / 1e9,
+                                     "g_gathers_per_s": (nnz / sec / 1e9) if gather else 0.0})
+            finally:
+                for st in sets:
+                    for b in st:
+                        b.free()
+    finally:
+        out.free()
+    return rows
+
+
 def render(gather: List[dict], stream: List[dict], device: str,
-           rowgather: List[dict] = ()) -> str:
+           rowgather: List[dict] = (), flat: List[dict] = ()) -> str:
     md = ["# Microbenchmarks (%s)" % device, "",
           "Written by `python -m tilegen_amd.microbench`; kernel times are medians of "
-          "dispatch-attached events.", "",
-          "## Random 8-byte gathers from an 800 KB (L2-resident) array", "",
-          "| kernel | active lanes / lanes routed through uniform loads | µs | G gathers/s | "
-          "G gather instructions/s |", "|---|---:|---:|---:|---:|"]
-    for r in gather:
-        md.append("| %s | %d | %.2f | %.1f | %.2f |" % (
-            r["kernel"], r["lanes_or_uniform"], r["us"], r["gathers_per_s"] / 1e9,
-            r["gather_instr_per_s"] / 1e9))
-    md += ["", "## Streaming 128-bit reads over cold copies", "",
-           "| MB | µs | GB/s | workgroups |", "|---:|---:|---:|---:|"]
-    for r in stream:
-        md.append("| %d | %.2f | %.0f | %d |" % (r["mb"], r["us"], r["gb_per_s"],
-                                                 r["workgroups"]))
+          "dispatch-attached events."]
+    if gather:
+        md += ["", "## Random 8-byte gathers from an 800 KB (L2-resident) array", "",
+               "| kernel | active lanes / lanes routed through uniform loads | µs | "
+               "G gathers/s | G gather instructions/s |", "|---|---:|---:|---:|---:|"]
+        for r in gather:
+            md.append("| %s | %d | %.2f | %.1f | %.2f |" % (
+                r["kernel"], r["lanes_or_uniform"], r["us"], r["gathers_per_s"] / 1e9,
+                r["gather_instr_per_s"] / 1e9))
+    if stream:
+        md += ["", "## Streaming 128-bit reads over cold copies", "",
+               "| MB | µs | GB/s | workgroups |", "|---:|---:|---:|---:|"]
+        for r in stream:
+            md.append("| %d | %.2f | %.0f | %d |" % (r["mb"], r["us"], r["gb_per_s"],
+                                                     r["workgroups"]))
     if rowgather:
         md += ["", "## Random 512-byte row gathers (SpMM's B rows: 100000 x 16 gathers, "
                "one 512-byte row written per 16)", "",
@@ -283,26 +373,46 @@ def render(gather: List[dict], stream: List[dict], device: str,
             md.append("| %.1f | %s | %.2f | %.2f | %.0f | %.0f |" % (
                 r["table_mb"], "cold (%d copies)" % r["copies"] if r["cold"] else "warm",
                 r["us"], r["g_rows_per_s"], r["gathered_gb_per_s"], r["written_gb_per_s"]))
+    if flat:
+        md += ["", "## c1's accesses without rows (c1's own indices and values, 16 nonzeros "
+               "per 8-lane group, no row pointers, LDS or barriers)", "",
+               "| inputs | x gathers | block | µs | GB/s streamed (indices, values, out) | "
+               "G gathers/s |", "|---|---|---:|---:|---:|---:|"]
+        for r in flat:
+            md.append("| %s | %s | %d | %.2f | %.0f | %s |" % (
+                "cold (%d copies)" % r["copies"] if r["cold"] else "warm",
+                "yes" if r["gather"] else "no", r["block"], r["us"], r["streamed_gb_per_s"],
+                "%.1f" % r["g_gathers_per_s"] if r["gather"] else "-"))
     return "\n".join(md) + "\n"
 
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="Gather and streaming-read microbenchmarks.")
     ap.add_argument("--out", default="results")
+    ap.add_argument("--only", choices=["flat"], default=None,
+                    help="run one probe and print its table (results/ is left as it is)")
     a = ap.parse_args(argv)
     if rt.device_count() < 1:
         print("microbench: no HIP device visible", file=sys.stderr)
         return 2
     dev = rt.device_info(0)
+    if a.only == "flat":
+        print(render([], [], dev["arch"], flat=flat_probe()), flush=True)
+        return 0
     g = gather_probe()
+    print("[microbench] gather done", flush=True)
     s = stream_probe()
+    print("[microbench] stream done", flush=True)
     rg = rowgather_probe()
+    print("[microbench] rowgather done", flush=True)
+    fl = flat_probe()
     os.makedirs(a.out, exist_ok=True)
     with open(os.path.join(a.out, "microbench.json"), "w") as fh:
-        json.dump({"device": dev, "gather": g, "stream": s, "rowgather": rg}, fh, indent=1)
+        json.dump({"device": dev, "gather": g, "stream": s, "rowgather": rg, "flat": fl}, fh,
+                  indent=1)
     with open(os.path.join(a.out, "microbench.md"), "w") as fh:
-        fh.write(render(g, s, "%s %s" % (dev["name"], dev["arch"]), rg))
-    print(render(g, s, dev["arch"], rg))
+        fh.write(render(g, s, "%s %s" % (dev["name"], dev["arch"]), rg, fl))
+    print(render(g, s, dev["arch"], rg, fl))
     return 0
 
 
