@@ -54,6 +54,9 @@ def _parse_config(text: str):
     vals = {}
     for part in text.replace(",", "/").split("/"):
         part = part.strip()
+        if part in ("nnz", "rows"):  # what a tile holds (merge-path windows or rows)
+            vals["balance"] = part
+            continue
         for key, name in (("TPR", "threads_per_row"), ("T", "tile_size"), ("U", "unroll"),
                           ("V", "vector_width"), ("B", "block_size")):
             if part.startswith(key) and part[len(key):].isdigit():
@@ -172,7 +175,9 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--case", default="c1")
-    ap.add_argument("--config", default=None, help="schedule override, e.g. T128/TPR8/U2/V1/B256")
+    ap.add_argument("--config", default=None,
+                    help="schedule override, e.g. T128/TPR8/U2/V1/B256 (append /nnz for "
+                         "merge-path windows)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="bound on the CPU baseline's timed calls")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")

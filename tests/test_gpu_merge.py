@@ -1,0 +1,99 @@
+"""GPU parity of the merge-path (balance "nnz") SpMV and fused_spmv_axpy.
+
+Each workgroup takes an equal share of rows plus nonzeros, finds its first and
+last rows with a search of the row pointers, sums the rows that begin in its
+share whole, and adds its piece of any row longer than a share to the scratch
+the last piece reads back.  The matrices put that logic at its edges: no
+nonzeros, one row, rows ending exactly at the last nonzero, a row spanning
+hundreds of windows (more than one wave of pieces to combine), long first and
+last rows, mostly empty rows, power-law and dense-row patterns, and more
+windows than the scratch holds (rows past it are summed whole).  Every result
+must meet the 1e-10 normwise bar against the C oracle and float64 SciPy, and
+launching again onto NaN-filled outputs must give the same bits (the piece
+order is fixed and every count is back at zero).  Launches go through
+``launch_<name>`` with device pointers.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests.test_gpu_parity import TOL, _check, _operands
+from tests.util import csr, ragged, rel_inf
+from tilegen_amd import codegen as cg
+from tilegen_amd.codegen import Config
+from tilegen_amd.matrices import make_baseline
+from tilegen_amd.schedules import MERGE_TEST_SCHEDULES, schedule_id
+from tilegen_amd.variant import Variant
+
+pytestmark = pytest.mark.gpu
+
+
+def _cases():
+    return {
+        "no_nonzeros": csr(100, 50, np.zeros(101, dtype=np.int64), [], []),
+        "single": csr(1, 1, [0, 1], [0], [2.5]),
+        "last_row_to_nnz_end": csr(3, 5, [0, 1, 2, 7], [0, 1, 0, 1, 2, 3, 4],
+                                   [1, 2, 3, 4, 5, 6, 7]),
+        "one_huge_row": ragged(4, 400, 30000, 2, long_rows=[(200, 25000)]),
+        "huge_first_and_last": ragged(5, 300, 9000, 5,
+                                      long_rows=[(0, 8000), (299, 7000), (150, 6)]),
+        "mostly_empty": ragged(3, 3000, 500, 3, empty_every=2, long_rows=[(7, 400)]),
+        "power_law": make_baseline("c3a", scale=0.05),
+        "dense_rows": make_baseline("c3b", scale=0.1),
+        "every_row_long": ragged(21, 200, 3000, 0, long_rows=[(r, 300 + r) for r in range(200)]),
+        "uniform": make_baseline("c1", scale=0.02),
+    }
+
+
+def _again_onto_nan(kernel, cfg, A, first):
+    """A second launch onto NaNs gives the same bits as the first."""
+    ops = _operands(kernel, A, 1)
+    out = Variant(kernel, cfg).run(A, out=np.full(A.shape[0], np.nan), **ops)
+    assert np.array_equal(out, first)
+
+
+@pytest.mark.parametrize("cfg", MERGE_TEST_SCHEDULES,
+                         ids=[schedule_id(c) for c in MERGE_TEST_SCHEDULES])
+@pytest.mark.parametrize("kernel", ["spmv", "fused_spmv_axpy"])
+def test_merge_path_matches_oracle(kernel, cfg, hip_ready):
+    for label, A in _cases().items():
+        print("[gpu] merge %s %s %s rows=%d nnz=%d" % (kernel, cfg.short(), label,
+                                                      A.shape[0], A.nnz), flush=True)
+        out = _check(kernel, cfg, A, K=1, label=label)
+        _again_onto_nan(kernel, cfg, A, out)
+
+
+def test_merge_path_more_windows_than_scratch(hip_ready):
+    """100000 windows (two rows each) against 65536 scratch slots: the long row
+    near the top is cut into pieces, the one near the bottom is summed whole by
+    the window it begins in."""
+    rows = 200_000
+    A = ragged(31, rows, 60_000, 1, long_rows=[(10, 5000), (rows - 900, 6000)])
+    cfg = Config(tile_size=2, threads_per_row=4, unroll=1, block_size=64, balance="nnz")
+    G = -(-rows // 2)
+    X = rows + A.nnz
+    D = -(-X // G)  # items per window
+    assert G > cg.MERGE_CAP
+    assert (rows - 900 + int(A.indptr[rows - 900 + 1]) - 1) // D >= cg.MERGE_CAP
+    assert (10 + int(A.indptr[11]) - 1) // D < cg.MERGE_CAP
+    print("[gpu] merge scratch capacity rows=%d nnz=%d windows=%d" % (rows, A.nnz, G),
+          flush=True)
+    out = _check("spmv", cfg, A, K=1, label="past_scratch")
+    _again_onto_nan("spmv", cfg, A, out)
+
+
+def test_merge_path_agrees_with_row_tiles(hip_ready):
+    """The same schedule with row tiles and with merge-path windows: both meet
+    the bar on the BASELINE skewed cases at a tenth of their size, and agree
+    with each other to it."""
+    for case_id, base in (("c3a", (64, 8, 2, 512)), ("c3b", (32, 32, 2, 1024))):
+        A = make_baseline(case_id, scale=0.1)
+        ops = _operands("spmv", A, 1)
+        T, tpr, U, B = base
+        rows = Variant("spmv", Config(tile_size=T, threads_per_row=tpr, unroll=U,
+                                      block_size=B)).run(A, **ops)
+        merge = Variant("spmv", Config(tile_size=T, threads_per_row=tpr, unroll=U,
+                                       block_size=B, balance="nnz")).run(A, **ops)
+        assert rel_inf(merge, rows) <= TOL, case_id

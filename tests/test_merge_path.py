@@ -1,0 +1,225 @@
+"""(CPU) The merge-path partition of the nnz-balanced SpMV kernels.
+
+``mp_search`` restates the device search ``tg_mp_search`` lane for lane (64
+probes per round, the same first-round pattern, clamping and bracket update);
+``partition`` restates the window set-up the emitter writes for every
+workgroup (window bounds, first/last row, the pieces of rows longer than a
+window, the rows summed whole).  The tests check them against what the
+mathematics fixes, on skewed, empty-row, single-row and no-nonzero matrices
+and on several grid sizes:
+
+* the search returns the exact lower bound ``numpy.searchsorted`` gives, its
+  probes stay inside the row-pointer array, and it ends within
+  ``2 + ceil(log63(rows + 1))`` rounds;
+* every nonzero of every row is summed exactly once: rows summed whole belong
+  to exactly one window, and the pieces of a cut row tile its nonzeros with no
+  gap or overlap, one piece per window from its first window to its last;
+* no window holds two pieces of the same kind (its two scratch slots), and no
+  window's work exceeds two windows' worth of items;
+* rows that reach past the scratch capacity are summed whole by their first
+  window and by no other.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from tests.util import ragged
+from tilegen_amd import codegen as cg
+from tilegen_amd.codegen import Config
+from tilegen_amd.matrices import make_baseline
+
+
+def mp_search(indptr, R: int, t: int, X: int):
+    """Lane-for-lane model of ``tg_mp_search``: (answer, rounds, probed rows)."""
+    g = int(float(t) * (float(R) / float(X))) if X > 0 else 0
+    qs = []
+    for l in range(64):
+        if l < 48:
+            qs.append(g - 24 + l)
+        else:
+            d = 32 << (2 * ((l - 48) >> 1))
+            qs.append(g + 24 + d if l & 1 else g - 24 - d)
+    lo, hi, rounds, probed = 0, R, 0, set()
+    while True:
+        rounds += 1
+        qs = [min(max(q, lo), hi) for q in qs]
+        probed.update(qs)
+        ge = [q + int(indptr[q]) >= t for q in qs]
+        a = max([lo - 1] + [q for q, g_ in zip(qs, ge) if not g_])
+        b = min([hi] + [q for q, g_ in zip(qs, ge) if g_])
+        lo, hi = a + 1, b
+        if lo >= hi:
+            return hi, rounds, probed
+        s = (hi - lo + 62) // 63
+        qs = [lo + l * s for l in range(64)]
+
+
+def lower_bound(indptr, R: int, t: int) -> int:
+    f = np.arange(R + 1, dtype=np.int64) + np.asarray(indptr[:R + 1], dtype=np.int64)
+    return min(int(np.searchsorted(f, t, side="left")), R)
+
+
+def partition(indptr, M: int, G: int, cap: int = cg.MERGE_CAP):
+    """The emitter's per-workgroup window set-up for every workgroup: a list of
+    (rows summed whole, pieces) with pieces as (row, begin, end, wf, wl, w)."""
+    nnz = int(indptr[M])
+    X = M + nnz
+    D = (X + G - 1) // G if X > G else 1
+    ip = lambda r: int(indptr[r]) if r >= 0 else 0  # noqa: E731
+    out = []
+    for w in range(G):
+        t0 = min(w * D, X)
+        t1 = min(t0 + D, X)
+        r0 = 0 if w == 0 else mp_search(indptr, M, t0, X)[0]
+        r1 = M if w == G - 1 else mp_search(indptr, M, t1, X)[0]
+        s2, s3, s4, s5 = ip(r0 - 1), ip(r0), ip(r1 - 1), ip(r1)
+        pc_in = r0 > 0 and s3 - s2 > D and (r0 - 1 + s3 - 1) // D < cap and r0 - 1 + s3 > t0
+        pc_out = r1 > r0 and s5 - s4 > D and (r1 - 1 + s5 - 1) // D < cap
+        r_own = r1 - 1 if pc_out else r1
+        pieces = []
+        for k, on in ((0, pc_in), (1, pc_out)):
+            if not on:
+                continue
+            row = r0 - 1 if k == 0 else r1 - 1
+            pb, pe = (s2, s3) if k == 0 else (s4, s5)
+            c0 = t0 - row if k == 0 and t0 - row > pb else pb
+            c1 = min(t1 - row, pe)
+            pieces.append((row, c0, c1, (row + pb) // D, (row + pe - 1) // D, w))
+        out.append((range(r0, r_own), pieces, D))
+    return out
+
+
+def check_partition(indptr, M: int, G: int, cap: int = cg.MERGE_CAP) -> dict:
+    parts = partition(indptr, M, G, cap)
+    D = parts[0][2]
+    whole = np.zeros(M, dtype=np.int64)
+    cut = {}
+    for w, (own, pieces, _) in enumerate(parts):
+        for r in own:
+            whole[r] += 1
+        kinds = [p[3] == w for p in pieces]
+        assert kinds.count(True) <= 1 and kinds.count(False) <= 1, (w, pieces)
+        # rows past the scratch capacity are summed whole, so they are left out
+        work = sum(int(indptr[r + 1] - indptr[r]) + 1 for r in own
+                   if indptr[r + 1] - indptr[r] <= D)
+        work += sum(p[2] - p[1] for p in pieces)
+        assert work <= 2 * D + 1, (w, work, D)
+        for p in pieces:
+            cut.setdefault(p[0], []).append(p)
+    for r, pcs in cut.items():
+        assert whole[r] == 0, r
+        rs, re = int(indptr[r]), int(indptr[r + 1])
+        pcs.sort(key=lambda p: p[5])
+        wf, wl = pcs[0][3], pcs[0][4]
+        assert all(p[3] == wf and p[4] == wl for p in pcs), pcs
+        assert [p[5] for p in pcs] == list(range(wf, wl + 1)), pcs
+        assert wl < cap and wl > wf
+        assert pcs[0][1] == rs and pcs[-1][2] == re, pcs
+        for a, b in zip(pcs, pcs[1:]):
+            assert a[2] == b[1] and a[1] < a[2], (a, b)
+    lens = np.diff(np.asarray(indptr[:M + 1], dtype=np.int64))
+    for r in range(M):
+        if r not in cut:
+            assert whole[r] == 1, (r, whole[r])
+            if lens[r] > D:  # a long row kept whole: its windows reach past the scratch
+                assert (r + int(indptr[r + 1]) - 1) // D >= cap
+    return {"D": D, "cut": len(cut), "max_pieces": max((len(v) for v in cut.values()), default=0)}
+
+
+def _cases():
+    yield "power_law", make_baseline("c3a", scale=0.05)
+    yield "dense_rows", make_baseline("c3b", scale=0.1)
+    yield "uniform", make_baseline("c1", scale=0.02)
+    yield "banded", make_baseline("c2", scale=0.02)
+    yield "mostly_empty", ragged(3, 3000, 500, 3, empty_every=2, long_rows=[(7, 400)])
+    yield "one_huge_row", ragged(4, 400, 30000, 2, long_rows=[(200, 25000)])
+    yield "huge_first_and_last", ragged(5, 300, 9000, 5,
+                                        long_rows=[(0, 8000), (299, 7000), (150, 6)])
+    yield "no_nonzeros", ragged(6, 100, 10, 0)
+    yield "single_row", ragged(7, 1, 5000, 0, long_rows=[(0, 4000)])
+
+
+@pytest.mark.parametrize("T", [1, 4, 16, 64, 1024])
+def test_partition_covers_every_nonzero_once(T):
+    seen_cut = 0
+    for label, A in _cases():
+        M = A.shape[0]
+        G = max(1, -(-M // T))
+        info = check_partition(A.indptr, M, G)
+        seen_cut += info["cut"]
+    if T <= 64:  # a window per 64 rows or fewer: the long rows above are cut
+        assert seen_cut > 0
+
+
+def test_search_is_the_exact_lower_bound():
+    rng = np.random.default_rng(11)
+    for label, A in _cases():
+        M = A.shape[0]
+        X = M + int(A.indptr[M])
+        bound = 2 + math.ceil(math.log(M + 1, 63))
+        for t in list(rng.integers(0, X + 2, size=60)) + [0, 1, X - 1, X, X + 1]:
+            t = int(t)
+            got, rounds, probed = mp_search(A.indptr, M, t, X)
+            assert got == lower_bound(A.indptr, M, t), (label, t)
+            assert min(probed) >= 0 and max(probed) <= M
+            assert rounds <= bound, (label, t, rounds)
+
+
+def test_uniform_rows_take_one_round():
+    """Rows of equal length: the proportional guess lands within the 48
+    consecutive probes, so a window's first row costs one row-pointer load."""
+    for A in (make_baseline("c1", scale=0.05), make_baseline("c2", scale=0.05)):
+        M = A.shape[0]
+        X = M + int(A.indptr[M])
+        G = -(-M // 16)
+        D = -(-X // G)
+        rounds = [mp_search(A.indptr, M, min(w * D, X), X)[1] for w in range(1, G)]
+        assert max(rounds) == 1, max(rounds)
+
+
+def test_rows_past_the_scratch_stay_whole():
+    A = ragged(8, 500, 6000, 4, long_rows=[(20, 3000), (480, 5000)])
+    full = check_partition(A.indptr, 500, 250)
+    assert full["cut"] == 2
+    small = check_partition(A.indptr, 500, 250, cap=100)  # only the first row's windows fit
+    assert small["cut"] == 1
+
+
+def test_config_balance_is_additive():
+    """balance leaves every reference schedule's hash and dict as they were."""
+    c = Config(tile_size=64, threads_per_row=8, unroll=2, block_size=512)
+    assert "balance" not in c.to_dict()
+    n = Config(tile_size=64, threads_per_row=8, unroll=2, block_size=512, balance="nnz")
+    assert n.to_dict()["balance"] == "nnz" and n.hash() != c.hash()
+    assert n.short() == c.short() + "/nnz"
+    assert Config(**n.to_dict()) == n
+
+
+def test_merge_source_and_refusals():
+    from tilegen_amd import dsl
+    ks = dsl.standard_kernels()
+    cfg = Config(tile_size=64, threads_per_row=8, unroll=2, block_size=512, balance="nnz")
+    for k in ("spmv", "fused_spmv_axpy"):
+        g = cg.generate(ks[k], cfg, backend="hip", write=False)
+        assert "tg_mp_search(indptr, row_lim, t0, X)" in g.source
+        assert "tg_mp_commit(wdx, wf, wl, t, &tot)" in g.source
+        tiling = [e for e in cg._passes.run_pipeline(ks[k], cfg, backend="hip").pass_log
+                  if e["pass"] == "tiling"][0]
+        assert "merge path" in tiling["action"]
+    # the row-tiled source is unchanged by the option's existence
+    rows = cg.generate(ks["spmv"], Config(tile_size=64, threads_per_row=8, unroll=2,
+                                          block_size=512), backend="hip", write=False)
+    assert "tg_mp_" not in rows.source
+    for k, c in (("spmm", Config(tile_size=16, threads_per_row=16, unroll=2, vector_width=2,
+                                 block_size=64, balance="nnz")),
+                 ("spmv", Config(tile_size=1, threads_per_row=8, block_size=128,
+                                 balance="nnz"))):
+        with pytest.raises(ValueError, match="balance 'nnz'"):
+            cg.generate(ks[k], c, backend="hip", write=False)
+    # the CPU backend ignores it (like threads_per_row and block_size)
+    cpu = cg.generate(ks["spmv"], cfg, backend="cpu", write=False)
+    assert "tg_mp_" not in cpu.source

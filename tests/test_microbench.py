@@ -58,9 +58,10 @@ def test_flat_kernel_compiles_and_renders():
           {"cold": False, "copies": 1, "gather": False, "block": 256, "nnz": 1600000,
            "us": 4.0, "streamed_bytes": 26400000, "streamed_gb_per_s": 6600.0,
            "g_gathers_per_s": 0.0}]
+    fl[1]["case"] = "c2"
     md = microbench.render([], [], "x", flat=fl)
-    assert "| cold (47 copies) | yes | 128 | 11.50 | 2296 | 139.1 |" in md
-    assert "| warm | no | 256 | 4.00 | 6600 | - |" in md
+    assert "| c1 | cold (47 copies) | yes | 128 | 11.50 | 2296 | 139.1 |" in md
+    assert "| c2 | warm | no | 256 | 4.00 | 6600 | - |" in md
 
 
 @pytest.mark.gpu
@@ -69,3 +70,6 @@ def test_flat_probe_runs(hip_ready):
     r = microbench.flat_probe(rotate_mb=64, iters=3, blocks=(256,))
     assert len(r) == 4 and all(x["us"] > 0 for x in r)
     assert [x["gather"] for x in r] == [True, False, True, False]
+    # c2's nonzero count is not a multiple of 16: the probe leaves the tail out
+    r2 = microbench.flat_probe(rotate_mb=64, iters=3, blocks=(256,), case="c2")
+    assert r2[0]["nnz"] % 16 == 0 and r2[0]["case"] == "c2"

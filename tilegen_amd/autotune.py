@@ -23,6 +23,7 @@ before it is timed, and only verified variants can win.
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 import itertools
 import json
 import os
@@ -60,6 +61,8 @@ BASELINE = Config(tile_size=32, threads_per_row=1, unroll=1, vector_width=1, blo
 
 _WAVE = 64
 _LDS_LIMIT = 64 * 1024
+# kernels whose schedules also come with merge-path windows (Config.balance)
+MERGE_KERNELS = ("spmv", "fused_spmv_axpy")
 ROTATE_BYTES = 640 << 20
 
 
@@ -159,6 +162,9 @@ def enumerate_configs(kernel: Optional[str] = None, K: int = 8
         cfg = Config(**dict(zip(keys, combo)))
         reason = illegal_reason(cfg) if kernel is None else illegal_reason_for(kernel, cfg, K)
         out.append((cfg, reason))
+    if kernel in MERGE_KERNELS:
+        # the same schedules with merge-path windows instead of row tiles
+        out += [(dataclasses.replace(c, balance="nnz"), r) for c, r in list(out)]
     return out
 
 
@@ -325,11 +331,13 @@ def _candidate_configs(kernel: str, K: int, budget: int, mode: str, rng: random.
         add(c)
     if mode == "coordinate":
         best = out[0]
-        for key in SEARCH_SPACE:
-            for value in SEARCH_SPACE[key]:
-                add(Config(**{**best.to_dict(), key: value}))
-                if len(out) >= budget:
-                    return out
+        steps = [(key, value) for key in SEARCH_SPACE for value in SEARCH_SPACE[key]]
+        if kernel in MERGE_KERNELS:
+            steps.append(("balance", "nnz"))
+        for key, value in steps:
+            add(Config(**{**best.to_dict(), key: value}))
+            if len(out) >= budget:
+                return out
         return out[:budget]
     if mode == "exhaustive":
         for c in pool:

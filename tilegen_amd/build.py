@@ -89,7 +89,7 @@ def warm_cache(verbose: bool = False) -> int:
     from .dsl import standard_kernels
     from .matrices import baseline_case
     from .passes import PASS_NAMES
-    from .schedules import TEST_KERNELS, TEST_SCHEDULES, TUNED
+    from .schedules import MERGE_TEST_SCHEDULES, TEST_KERNELS, TEST_SCHEDULES, TUNED
     from .verify import compile_generated
 
     kernels = standard_kernels()
@@ -101,6 +101,9 @@ def warm_cache(verbose: bool = False) -> int:
             todo.append((name, cfg, ()))
         todo.append((name, Config(tile_size=32, threads_per_row=4, unroll=2, vector_width=1,
                                   block_size=256, inject_bug=True), ()))
+    for name in ("spmv", "fused_spmv_axpy"):
+        for cfg in MERGE_TEST_SCHEDULES:
+            todo.append((name, cfg, ()))
     for name, cases in DEFAULT_CASES.items():
         for case_id in cases:
             todo += [(name, TUNED[case_id], skip) for skip in [()] + [(p,) for p in PASS_NAMES]]

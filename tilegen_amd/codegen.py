@@ -88,7 +88,12 @@ class Config:
     """Flat schedule request; the passes lower it into the schedule IR.
 
     tile_size T (rows per workgroup), threads_per_row TPR, unroll U,
-    vector_width V, block_size B (lanes per workgroup).
+    vector_width V, block_size B (lanes per workgroup).  ``balance`` is what
+    a tile holds on the HIP backend: ``"rows"`` (T consecutive rows) or
+    ``"nnz"`` (an equal share of rows plus nonzeros, about T rows' worth, for
+    SpMV-shaped kernels; see ``_hip_scalar_reduce``).  It has no counterpart in
+    the reference and is left out of ``to_dict``/``hash`` at its default, so
+    every reference schedule keeps its name.
     """
 
     tile_size: int = 32
@@ -98,24 +103,32 @@ class Config:
     block_size: int = 256
     dtype: str = "f64"
     inject_bug: bool = False
+    balance: str = "rows"
 
     def to_dict(self) -> Dict[str, Any]:
-        return {"tile_size": self.tile_size, "threads_per_row": self.threads_per_row,
-                "unroll": self.unroll, "vector_width": self.vector_width,
-                "block_size": self.block_size, "dtype": self.dtype,
-                "inject_bug": self.inject_bug}
+        d = {"tile_size": self.tile_size, "threads_per_row": self.threads_per_row,
+             "unroll": self.unroll, "vector_width": self.vector_width,
+             "block_size": self.block_size, "dtype": self.dtype,
+             "inject_bug": self.inject_bug}
+        if self.balance != "rows":
+            d["balance"] = self.balance
+        return d
 
     def hash(self) -> str:
         """sha1 of ``T|TPR|U|V|B|dtype|bug``, 10 hex digits (the reference's
-        closed form, ``codegen.py:82-87``, so cache names line up)."""
+        closed form, ``codegen.py:82-87``, so cache names line up); a
+        non-default ``balance`` is appended as ``|<balance>``."""
         key = "%d|%d|%d|%d|%d|%s|%d" % (self.tile_size, self.threads_per_row, self.unroll,
                                         self.vector_width, self.block_size, self.dtype,
                                         int(self.inject_bug))
+        if self.balance != "rows":
+            key += "|" + self.balance
         return hashlib.sha1(key.encode()).hexdigest()[:10]
 
     def short(self) -> str:
-        return "T%d/TPR%d/U%d/V%d/B%d" % (self.tile_size, self.threads_per_row,
-                                          self.unroll, self.vector_width, self.block_size)
+        return "T%d/TPR%d/U%d/V%d/B%d%s" % (self.tile_size, self.threads_per_row,
+                                            self.unroll, self.vector_width, self.block_size,
+                                            "/nnz" if self.balance == "nnz" else "")
 
 
 @dataclass
@@ -133,18 +146,22 @@ class Lowering:
     block_size: int = 256
     parallel: bool = False
     tiled: bool = False
+    balance: str = "rows"
 
     def to_dict(self) -> Dict[str, Any]:
-        return {"tile": self.tile, "threads_per_row": self.threads_per_row,
-                "unroll": self.unroll, "vector_width": self.vector_width,
-                "block_size": self.block_size, "parallel": self.parallel}
+        d = {"tile": self.tile, "threads_per_row": self.threads_per_row,
+             "unroll": self.unroll, "vector_width": self.vector_width,
+             "block_size": self.block_size, "parallel": self.parallel}
+        if self.balance != "rows":
+            d["balance"] = self.balance
+        return d
 
 
 def _lowering(kernel: Kernel) -> Lowering:
     low = Lowering()
     for t in kernel.schedule:
         if isinstance(t, Tile):
-            low.tile, low.tiled = t.size, True
+            low.tile, low.tiled, low.balance = t.size, True, t.by
         elif isinstance(t, ThreadsPerRow):
             low.threads_per_row = t.k
         elif isinstance(t, Unroll):
@@ -559,6 +576,8 @@ def _cpu_body(kernel: Kernel, config: Config, plan: Plan, low: Lowering) -> str:
 # --------------------------------------------------------------------------- #
 def _transform_text(t) -> str:
     if isinstance(t, Tile):
+        if t.by != "rows":
+            return "Tile(%s,%d,%s)" % (t.index.name, t.size, t.by)
         return "Tile(%s,%d)" % (t.index.name, t.size)
     if isinstance(t, Split):
         return "Split(%s,%d)" % (t.index.name, t.factor)
@@ -690,6 +709,9 @@ def _check_hip_schedule(plan: Plan, low: Lowering) -> None:
         raise ValueError("unroll must be in 1..16, got %d" % low.unroll)
     if low.tiled and low.tile > 4096:
         raise ValueError("tile_size %d exceeds 4096 rows per workgroup" % low.tile)
+    if low.balance == "nnz" and not (low.tiled and plan.kind == "scalar_reduce"):
+        raise ValueError("balance 'nnz' needs a tiled kernel that reduces over each row "
+                         "(SpMV-shaped); %s %s" % (plan.kind, "untiled" if not low.tiled else ""))
 
 
 def _long_row_test(length: str, long_: int, huge: int) -> str:
@@ -716,8 +738,141 @@ def _tile_stats(w: _W, TR: int) -> None:
     w("const tg_i64 t_nnz = s_tnnz;")
 
 
+# Merge-path windows (balance "nnz"): windows up to MERGE_CAP have scratch slots
+# for the pieces of rows longer than a window; rows reaching past them are summed
+# whole by the window they begin in.
+MERGE_CAP = 65536
+
+
+def _merge_decls(pre: _W) -> None:
+    """File-scope search, scratch and combine of the merge-path SpMV."""
+    pre(r"""// Merge path: row r occupies items r + indptr[r] .. r + indptr[r + 1] (its
+// nonzeros, then one item that ends it); the launch's items are cut into one
+// window per workgroup.
+//
+// Smallest r in [0, R] with r + indptr[r] >= t (R when there is none).  Run by
+// all 64 lanes of one wave, one row pointer per lane per round.  The first round
+// probes 48 consecutive rows around the proportional guess and 16 rows at
+// growing distances either side of it; each later round probes 64 evenly spaced
+// rows of the bracket left, so the bracket shrinks at least 63-fold per round.
+__device__ tg_i64 tg_mp_search(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 t, tg_i64 X) {
+  const int l = threadIdx.x & 63;
+  const tg_i64 g = X > 0 ? (tg_i64)((double)t * ((double)R / (double)X)) : 0;
+  tg_i64 q;
+  if (l < 48) {
+    q = g - 24 + l;
+  } else {
+    const tg_i64 d = (tg_i64)32 << (2 * ((l - 48) >> 1));
+    q = (l & 1) ? g + 24 + d : g - 24 - d;
+  }
+  tg_i64 lo = 0, hi = R;
+  #pragma unroll 1
+  for (;;) {
+    q = q < lo ? lo : (q > hi ? hi : q);
+    const bool ge = q + indptr[q] >= t;
+    tg_i64 a = ge ? lo - 1 : q;   // rows known to start before t
+    tg_i64 b = ge ? q : hi;       // rows known to start at or after t
+    #pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+      const tg_i64 a2 = tg_lane_bcast(a, l ^ m), b2 = tg_lane_bcast(b, l ^ m);
+      a = a2 > a ? a2 : a;
+      b = b2 < b ? b2 : b;
+    }
+    lo = a + 1;
+    hi = b;
+    if (lo >= hi) return hi;
+    q = lo + (tg_i64)l * ((hi - lo + 62) / 63);
+  }
+}
+
+// Partial sums of the pieces of rows cut at window edges, two per window w: the
+// piece of the row that begins in w (slot 2w + 1) and of the row that began
+// before it (slot 2w); and per first window, the number of pieces finished.
+// The last piece in zeroes the count, so every launch starts from zero.  Only
+// device-scope atomics touch these; launches that overlap on one device race.
+__device__ unsigned long long tg_mp_part[%(P)d];
+__device__ unsigned int tg_mp_cnt[%(C)d];
+
+// The value must be in a register (so the atomic that produced it has returned)
+// before any later memory operation is issued.
+__device__ __forceinline__ void tg_mp_wait(unsigned long long v) {
+  asm volatile("" :: "v"(v) : "memory");
+}
+
+// Wave: record window w's piece t of the row whose pieces lie in windows
+// wf..wl.  Lane 0 swaps the partial into its slot and, once that swap has
+// returned, counts the piece in; the piece that completes the count reads every
+// partial back (swapping in zeros), sums them in window order with a fixed
+// reduction tree, zeroes the count and returns true with the sum in *tot.
+__device__ bool tg_mp_commit(tg_i64 w, tg_i64 wf, tg_i64 wl, double t, double* tot) {
+  const int l = threadIdx.x & 63;
+  unsigned seen = 0;
+  if (l == 0) {
+    tg_mp_wait(__hip_atomic_exchange(tg_mp_part + 2 * w + (w == wf ? 1 : 0),
+                                     (unsigned long long)__double_as_longlong(t),
+                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    seen = __hip_atomic_fetch_add(tg_mp_cnt + wf, 1u, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+  }
+  seen = (unsigned)__shfl((int)seen, 0);
+  if ((tg_i64)seen + 1 != wl - wf + 1) return false;
+  double sum = 0.0;
+  #pragma unroll 1
+  for (tg_i64 base = wf; base <= wl; base += 64) {
+    const tg_i64 v = base + l;
+    double p = 0.0;
+    if (v <= wl)
+      p = __longlong_as_double((long long)__hip_atomic_exchange(
+          tg_mp_part + 2 * v + (v == wf ? 1 : 0), 0ull, __ATOMIC_RELAXED,
+          __HIP_MEMORY_SCOPE_AGENT));
+    sum += tg_segsum<64>(p);
+  }
+  if (l == 0)
+    (void)__hip_atomic_exchange(tg_mp_cnt + wf, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  *tot = sum;
+  return true;
+}
+""" % {"P": 2 * MERGE_CAP, "C": MERGE_CAP})
+
+
+def _merge_window(w: _W, TR: int, WAVES: int) -> None:
+    """This workgroup's merge-path window, its rows and its row pieces
+    (defines r0, r1, r_own, pc_in, pc_out, s_win, wdx, D, t0, t1)."""
+    w("// merge-path window of this workgroup: items [t0, t1) of row_lim + nnz")
+    w("__shared__ tg_i64 s_win[6];  // r0, r1, indptr[r0 - 1], indptr[r0], indptr[r1 - 1], indptr[r1]")
+    w("const tg_i64 G = gridDim.x, wdx = blockIdx.x;")
+    w("const tg_i64 X = row_lim + nnz;")
+    w("const tg_i64 D = X > G ? (X + G - 1) / G : 1;  // items per window")
+    w("const tg_i64 t0 = wdx * D < X ? wdx * D : X;")
+    w("const tg_i64 t1 = t0 + D < X ? t0 + D : X;")
+    w("// first and last rows: the first row beginning at or after t0 (t1)")
+    w.open("if (threadIdx.x < 64)")
+    w("const tg_i64 a = wdx == 0 ? 0 : tg_mp_search(indptr, row_lim, t0, X);")
+    w("if (threadIdx.x == 0) s_win[0] = a;")
+    w("if (threadIdx.x < 2) s_win[2 + threadIdx.x] = a - 1 + (tg_i64)threadIdx.x >= 0 ? "
+      "indptr[a - 1 + threadIdx.x] : 0;")
+    w.close()
+    sel = "threadIdx.x >= 64 && threadIdx.x < 128" if WAVES > 1 else "threadIdx.x < 64"
+    w.open("if (%s)" % sel)
+    w("const tg_i64 b = wdx == G - 1 ? row_lim : tg_mp_search(indptr, row_lim, t1, X);")
+    w("const int l = threadIdx.x & 63;")
+    w("if (l == 0) s_win[1] = b;")
+    w("if (l < 2) s_win[4 + l] = b - 1 + l >= 0 ? indptr[b - 1 + l] : 0;")
+    w.close()
+    w("__syncthreads();")
+    w("const tg_i64 r0 = s_win[0], r1 = s_win[1];")
+    w("// a row longer than a window is cut at the window edges when every window it")
+    w("// reaches has scratch slots (below %d); this window holds a piece of the row that" % MERGE_CAP)
+    w("// began before it, if that row reaches into it, and of its own last row")
+    w("const bool pc_in = r0 > 0 && s_win[3] - s_win[2] > D && "
+      "(r0 - 1 + s_win[3] - 1) / D < %d && r0 - 1 + s_win[3] > t0;" % MERGE_CAP)
+    w("const bool pc_out = r1 > r0 && s_win[5] - s_win[4] > D && "
+      "(r1 - 1 + s_win[5] - 1) / D < %d;" % MERGE_CAP)
+    w("const tg_i64 r_own = pc_out ? r1 - 1 : r1;  // rows summed whole, %d at a time" % TR)
+
+
 def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeometry,
-                       out_name: str) -> None:
+                       out_name: str, pre: Optional[_W] = None) -> None:
     """y[row] = final(sum over the row's nonzeros of value_expr).
 
     Tiled variants also balance skewed rows without any preprocessing: a row
@@ -728,6 +883,15 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     tier: rows over 2 group steps and up to 4 wave steps go to a second list
     whose rows the waves share out, one row per wave at a time, reduced within
     the wave (no barrier); only rows past that go to the workgroup.
+
+    With ``balance == "nnz"`` the workgroups split the merge path (every row
+    counts one item plus one per nonzero) into equal windows, one per T rows
+    of extent, instead of taking T rows each.  Workgroup w finds its window's
+    first and last rows with a 64-wide search of the row pointers, then runs
+    the body above over the rows whose first nonzero lies in its window, T
+    rows at a time.  A row longer than a window is cut at the window edges;
+    each window sums its piece with the whole workgroup and the piece that
+    finishes last adds the pieces up in window order (``_merge_decls``).
     """
     B, TPR = geo.block, max(1, low.threads_per_row)
     U = max(1, low.unroll)
@@ -746,11 +910,23 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     if wave_tier:
         MED = 2 * STEP
         WLONG = 4 * WAVE * U
+    merge = coop and low.balance == "nnz"
+    if merge:
+        if pre is None:
+            raise ValueError("merge-path tiles need file-scope declarations")
+        _merge_decls(pre)
+        # a window holds about T rows' worth of items but may hold several times
+        # T short rows; a batch is at least one row per lane group
+        TR = max(TR, SLOTS)
+        R = (TR + SLOTS - 1) // SLOTS
     row = plan.row_idx.name
     col = plan.col_idx.name
 
-    w("const tg_i64 row_end = %s;" % bound)
-    w("const tg_i64 row0 = (tg_i64)blockIdx.x * %d;" % TR)
+    if merge:
+        w("const tg_i64 row_lim = %s;  // rows this launch writes" % bound)
+    else:
+        w("const tg_i64 row_end = %s;" % bound)
+        w("const tg_i64 row0 = (tg_i64)blockIdx.x * %d;" % TR)
     w("const int lane = threadIdx.x %% %d;" % TPR)
     w("const int slot = threadIdx.x / %d;" % TPR)
     if U % 2 == 0:
@@ -767,6 +943,10 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
             w("__shared__ int s_med[%d];    // rows left to one wave each" % TR)
             w("__shared__ int s_nmed;")
         w("__shared__ double s_red[%d];" % WAVES)
+        if merge:
+            _merge_window(w, TR, WAVES)
+            w.open("for (tg_i64 row0 = r0; row0 < r_own; row0 += %d)" % TR)
+            w("const tg_i64 row_end = row0 + %d < r_own ? row0 + %d : r_own;" % (TR, TR))
         w("if (threadIdx.x == 0) { s_nlong = 0;%s }" % (" s_nmed = 0;" if wave_tier else ""))
         w.open("for (int t = threadIdx.x; t <= %d; t += %d)" % (TR, B))
         w("const tg_i64 r = row0 + t;")
@@ -931,6 +1111,42 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     env = _Env({row: "row"}, acc="t")
     w("__builtin_nontemporal_store(%s, %s + %s);" % (
         _cexpr(plan.final_expr, env), out_name, _offset(plan.out_tensor, plan.out.indices, env)))
+    w.close()
+    w("__syncthreads();")
+    w.close()
+    if not merge:
+        return
+    w("__syncthreads();  // the next batch rewrites s_ptr and the row lists")
+    w.close()
+    w("// pieces of rows longer than a window: the one that began before this")
+    w("// window (k = 0) and the one that begins in it and runs past its end (k = 1)")
+    w("#pragma unroll 1")
+    w.open("for (int k = 0; k < 2; ++k)")
+    w("if (!(k == 0 ? pc_in : pc_out)) continue;")
+    w("const tg_i64 row = k == 0 ? r0 - 1 : r1 - 1;")
+    w("const tg_i64 pb = k == 0 ? s_win[2] : s_win[4], pe = k == 0 ? s_win[3] : s_win[5];")
+    w("const tg_i64 c0 = k == 0 && t0 - row > pb ? t0 - row : pb;")
+    w("const tg_i64 c1 = t1 - row < pe ? t1 - row : pe;")
+    w("double cacc = 0.0;")
+    w("#pragma unroll 1")
+    w.open("for (tg_i64 q = (c0 & ~(tg_i64)%d) + (tg_i64)threadIdx.x * %d; q < c1; q += %d)"
+           % (ALIGN - 1, U, B * U))
+    step("q", "c0", "c1", "cacc")
+    w.close()
+    w("cacc = tg_segsum<64>(cacc);")
+    w("if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = cacc;")
+    w("__syncthreads();")
+    w.open("if (threadIdx.x < 64)")
+    w("double t = 0.0;")
+    w("#pragma unroll")
+    w("for (int v = 0; v < %d; ++v) t += s_red[v];" % WAVES)
+    w("const tg_i64 wf = (row + pb) / D, wl = (row + pe - 1) / D;  // its first/last window")
+    w("double tot;")
+    w.open("if (tg_mp_commit(wdx, wf, wl, t, &tot) && threadIdx.x == 0)")
+    env = _Env({row: "row"}, acc="tot")
+    w("__builtin_nontemporal_store(%s, %s + %s);" % (
+        _cexpr(plan.final_expr, env), out_name, _offset(plan.out_tensor, plan.out.indices, env)))
+    w.close()
     w.close()
     w("__syncthreads();")
     w.close()
@@ -1431,6 +1647,7 @@ def _hip_kernel_text(kernel: Kernel, config: Config, plan: Plan, low: Lowering,
                      args: List[Tuple[str, str]], geo: LaunchGeometry) -> str:
     bound = "(%s - 1)" % plan.row_extent if config.inject_bug else plan.row_extent
     out_name = plan.out_tensor.name
+    pre = _W()  # file-scope declarations the kernel needs
     w = _W()
     w("extern \"C\" __global__ __launch_bounds__(%d)" % geo.block)
     w.open("void %s_kernel(%s)" % (kernel.name, _hip_decls(args)))
@@ -1438,7 +1655,7 @@ def _hip_kernel_text(kernel: Kernel, config: Config, plan: Plan, low: Lowering,
         if not plan.reduce_is_compressed:
             raise NotImplementedError("HIP scalar_reduce needs the reduction over the "
                                       "compressed index")
-        _hip_scalar_reduce(w, plan, low, bound, geo, out_name)
+        _hip_scalar_reduce(w, plan, low, bound, geo, out_name, pre=pre)
     elif plan.kind == "row_dense_out":
         kext = _extent_for(plan, plan.inner_out[0].name)
         _hip_row_dense_out(w, plan, low, bound, geo, out_name, _dense_name(plan, 0), kext)
@@ -1451,12 +1668,15 @@ def _hip_kernel_text(kernel: Kernel, config: Config, plan: Plan, low: Lowering,
     else:  # pragma: no cover
         raise NotImplementedError(plan.kind)
     w.close()
-    return w.text()
+    return pre.text() + ("\n" if pre.lines else "") + w.text()
 
 
 def emit_hip(kernel: Kernel, config: Config) -> str:
     """Device translation unit of a lowered kernel (hipRTC input)."""
     plan, low = _plan(kernel), _lowering(kernel)
+    if config.balance == "nnz" and not low.tiled:
+        raise ValueError("balance 'nnz' needs a tile (tile_size > 1); %s is untiled"
+                         % config.short())
     _check_hip_schedule(plan, low)
     _sig, args, _info = abi_of(kernel)
     geo = launch_geometry(plan, low)

@@ -213,6 +213,9 @@ class Transform:
 class Tile(Transform):
     index: Index = None  # type: ignore[assignment]
     size: int = 0
+    #: what a tile holds: ``rows`` (``size`` consecutive rows) or ``nnz`` (an equal
+    #: share of rows plus nonzeros, about ``size`` rows' worth: merge-path windows)
+    by: str = "rows"
     kind: ClassVar[str] = "tile"
 
 
@@ -456,6 +459,8 @@ def _check_transform(t: Transform, known: set) -> None:
                              % (t.kind, ix.name))
     if isinstance(t, Tile) and t.size <= 0:
         raise ValueError("transform %r factor/size must be > 0" % t.kind)
+    if isinstance(t, Tile) and t.by not in ("rows", "nnz"):
+        raise ValueError("tile 'by' must be 'rows' or 'nnz', got %r" % t.by)
     if isinstance(t, Split) and t.factor <= 0:
         raise ValueError("transform %r factor/size must be > 0" % t.kind)
     if isinstance(t, Unroll) and t.factor <= 0:
@@ -573,6 +578,8 @@ def _loop_nest_lines(kernel: Kernel) -> List[str]:
 
 def _transform_text(t: Transform) -> str:
     if isinstance(t, Tile):
+        if t.by != "rows":
+            return "Tile(%s, %d, by=%s)" % (t.index.name, t.size, t.by)
         return "Tile(%s, %d)" % (t.index.name, t.size)
     if isinstance(t, Split):
         return "Split(%s, %d)" % (t.index.name, t.factor)
@@ -646,6 +653,8 @@ def _transform_dump(t: Transform) -> Dict[str, Any]:
     out: Dict[str, Any] = {"kind": t.kind}
     if isinstance(t, Tile):
         out.update(index={"name": t.index.name}, size=t.size)
+        if t.by != "rows":
+            out.update(by=t.by)
     elif isinstance(t, (Split, Unroll)):
         out.update(index={"name": t.index.name}, factor=t.factor)
     elif isinstance(t, Parallelize):
@@ -663,7 +672,7 @@ def _transform_load(d: Dict[str, Any]) -> Transform:
     kind = d["kind"]
     ix = Index(d["index"]["name"]) if "index" in d else None
     if kind == "tile":
-        return Tile(ix, d["size"])
+        return Tile(ix, d["size"], d.get("by", "rows"))
     if kind == "split":
         return Split(ix, d["factor"])
     if kind == "parallelize":

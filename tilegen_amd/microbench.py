@@ -21,12 +21,13 @@ rowgather
     Infinity Cache) and from a 3.2 MB one, with one 512-byte row written per
     16 gathered, cold (table copies rotated) and warm.
 flat
-    c1's SpMV accesses without its rows: the c1 matrix's own ``indices`` and
-    ``data`` streamed with one 128-bit load of each per lane, ``x`` gathered at
-    those indices, 8 lanes summing 16 products and one double stored per 16,
-    with no row pointers, LDS or barriers.  Cold (every array rotated) and
-    warm, with the gathers and without them (the stream alone): the floor for
-    the bytes and gathers c1 makes, against which the row logic is measured.
+    A SpMV case's accesses without its rows (c1 and c2 by default): the
+    matrix's own ``indices`` and ``data`` streamed with one 128-bit load of
+    each per lane, ``x`` gathered at those indices, 8 lanes summing 16
+    products and one double stored per 16, with no row pointers, LDS or
+    barriers.  Cold (every array rotated) and warm, with the gathers and
+    without them (the stream alone): the floor for the bytes and gathers the
+    case makes, against which the row logic is measured.
 
 ``python -m tilegen_amd.microbench --out results`` writes ``microbench.json``
 and ``microbench.md``.
@@ -290,20 +291,22 @@ def rowgather_probe(table_rows=(100_000, 6_250), n_groups: int = 100_000, per: i
     return rows
 
 
-def flat_probe(rotate_mb: int = 1280, iters: int = 100, blocks=(128, 256)) -> List[dict]:
-    """c1's indices/data/x accesses with no row structure (see the module
-    docstring), on the BASELINE c1 matrix itself."""
+def flat_probe(rotate_mb: int = 1280, iters: int = 100, blocks=(128, 256),
+               case: str = "c1") -> List[dict]:
+    """A SpMV case's indices/data/x accesses with no row structure (see the
+    module docstring), on that BASELINE matrix itself.  The nonzeros are taken
+    in groups of 16; a tail of fewer than 16 is left out."""
     from .matrices import baseline_operands, make_baseline
     fn = _load(_FLAT_SRC, ["mb_flat"])["mb_flat"]
-    A = make_baseline("c1")
+    A = make_baseline(case)
     M, N = A.shape
-    nnz = int(A.nnz)
-    if nnz % 16:
-        raise ValueError("the flat probe needs a multiple of 16 nonzeros, got %d" % nnz)
-    indices = np.ascontiguousarray(A.indices, dtype=np.int64)
+    nnz = int(A.nnz) // 16 * 16
+    if nnz == 0:
+        raise ValueError("the flat probe needs at least 16 nonzeros")
+    indices = np.ascontiguousarray(A.indices[:nnz], dtype=np.int64)
     if indices.min() < 0 or indices.max() >= N:  # every gather stays inside x
         raise AssertionError("index out of range")
-    data = np.ascontiguousarray(A.data, dtype=np.float64)
+    data = np.ascontiguousarray(A.data[:nnz], dtype=np.float64)
     x = baseline_operands("spmv", M, N, 1)["x"]
     n_groups = nnz // 16
     per_copy = indices.nbytes + data.nbytes + x.nbytes
@@ -331,7 +334,8 @@ def flat_probe(rotate_mb: int = 1280, iters: int = 100, blocks=(128, 256)) -> Li
                             raise AssertionError("mb_flat result off by %.3e" % err)
                         sec = float(np.median(kms)) * 1e-3
                         streamed = indices.nbytes + data.nbytes + n_groups * 8
-                        rows.append({"cold": cold, "copies": copies, "gather": bool(gather),
+                        rows.append({"case": case, "cold": cold, "copies": copies,
+                                     "gather": bool(gather),
                                      "block": block, "nnz": nnz, "us": sec * 1e6,
                                      "streamed_bytes": streamed,
                                      "streamed_gb_per_s": streamed / sec / 1e9,
@@ -374,13 +378,13 @@ def render(gather: List[dict], stream: List[dict], device: str,
                 r["table_mb"], "cold (%d copies)" % r["copies"] if r["cold"] else "warm",
                 r["us"], r["g_rows_per_s"], r["gathered_gb_per_s"], r["written_gb_per_s"]))
     if flat:
-        md += ["", "## c1's accesses without rows (c1's own indices and values, 16 nonzeros "
-               "per 8-lane group, no row pointers, LDS or barriers)", "",
-               "| inputs | x gathers | block | µs | GB/s streamed (indices, values, out) | "
-               "G gathers/s |", "|---|---|---:|---:|---:|---:|"]
+        md += ["", "## SpMV accesses without rows (the case's own indices and values, 16 "
+               "nonzeros per 8-lane group, no row pointers, LDS or barriers)", "",
+               "| case | inputs | x gathers | block | µs | GB/s streamed (indices, values, out) | "
+               "G gathers/s |", "|---|---|---|---:|---:|---:|---:|"]
         for r in flat:
-            md.append("| %s | %s | %d | %.2f | %.0f | %s |" % (
-                "cold (%d copies)" % r["copies"] if r["cold"] else "warm",
+            md.append("| %s | %s | %s | %d | %.2f | %.0f | %s |" % (
+                r.get("case", "c1"), "cold (%d copies)" % r["copies"] if r["cold"] else "warm",
                 "yes" if r["gather"] else "no", r["block"], r["us"], r["streamed_gb_per_s"],
                 "%.1f" % r["g_gathers_per_s"] if r["gather"] else "-"))
     return "\n".join(md) + "\n"
@@ -391,13 +395,17 @@ def main(argv=None) -> int:
     ap.add_argument("--out", default="results")
     ap.add_argument("--only", choices=["flat"], default=None,
                     help="run one probe and print its table (results/ is left as it is)")
+    ap.add_argument("--flat-cases", default="c1,c2",
+                    help="SpMV cases the flat probe runs on (comma-separated)")
     a = ap.parse_args(argv)
     if rt.device_count() < 1:
         print("microbench: no HIP device visible", file=sys.stderr)
         return 2
     dev = rt.device_info(0)
+    cases = [c for c in a.flat_cases.split(",") if c]
     if a.only == "flat":
-        print(render([], [], dev["arch"], flat=flat_probe()), flush=True)
+        print(render([], [], dev["arch"], flat=[r for c in cases for r in flat_probe(case=c)]),
+              flush=True)
         return 0
     g = gather_probe()
     print("[microbench] gather done", flush=True)
@@ -405,7 +413,7 @@ def main(argv=None) -> int:
     print("[microbench] stream done", flush=True)
     rg = rowgather_probe()
     print("[microbench] rowgather done", flush=True)
-    fl = flat_probe()
+    fl = [r for c in cases for r in flat_probe(case=c)]
     os.makedirs(a.out, exist_ok=True)
     with open(os.path.join(a.out, "microbench.json"), "w") as fh:
         json.dump({"device": dev, "gather": g, "stream": s, "rowgather": rg, "flat": fl}, fh,

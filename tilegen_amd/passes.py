@@ -175,7 +175,16 @@ def tiling(kernel: Kernel) -> Kernel:
         _remove_transforms(kernel, Tile, same)
         _log(kernel, "tiling", "tile_size <= 1; no tiling applied")
         return kernel
-    _set_transform(kernel, Tile, same, Tile(outer, size))
+    balance = getattr(getattr(kernel, "_config", None), "balance", "rows") or "rows"
+    _set_transform(kernel, Tile, same, Tile(outer, size, balance))
+    if balance == "nnz":
+        _log(kernel, "tiling",
+             "split '%s' into windows of equal rows-plus-nonzeros (merge path), one per %d "
+             "rows of extent; rows longer than a window are shared by the windows they span"
+             % (outer.name, size),
+             "for %s in 0..extent" % outer.name,
+             "for window w: for %s whose first nonzero is in w: ..." % outer.name)
+        return kernel
     _log(kernel, "tiling",
          "strip-mined '%s' into tiles of %d rows ('%s_o' over tiles, '%s_i' within)"
          % (outer.name, size, outer.name, outer.name),

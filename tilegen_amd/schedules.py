@@ -52,7 +52,21 @@ TEST_SCHEDULES: List[Config] = [
 
 TEST_KERNELS = ["spmv", "spmm", "sddmm", "fused_spmv_axpy", "axpy"]
 
+# Swept by the GPU parity tests of the merge-path (balance "nnz") SpMV and
+# fused_spmv_axpy: one wave (both window searches in one wave) and sixteen,
+# windows of about 2 to 256 rows, every lane-group width tier.
+MERGE_TEST_SCHEDULES: List[Config] = [
+    Config(tile_size=16, threads_per_row=8, unroll=2, block_size=128, balance="nnz"),
+    Config(tile_size=64, threads_per_row=8, unroll=2, block_size=512, balance="nnz"),
+    Config(tile_size=32, threads_per_row=32, unroll=2, block_size=1024, balance="nnz"),
+    Config(tile_size=2, threads_per_row=4, unroll=1, block_size=64, balance="nnz"),
+    Config(tile_size=128, threads_per_row=1, unroll=1, block_size=64, balance="nnz"),
+    Config(tile_size=256, threads_per_row=64, unroll=4, block_size=256, balance="nnz"),
+    Config(tile_size=8, threads_per_row=16, unroll=3, block_size=256, balance="nnz"),
+]
+
 
 def schedule_id(c: Config) -> str:
-    return "T%d-TPR%d-U%d-V%d-B%d" % (c.tile_size, c.threads_per_row, c.unroll,
-                                      c.vector_width, c.block_size)
+    return "T%d-TPR%d-U%d-V%d-B%d%s" % (c.tile_size, c.threads_per_row, c.unroll,
+                                        c.vector_width, c.block_size,
+                                        "-nnz" if c.balance == "nnz" else "")
