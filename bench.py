@@ -54,7 +54,7 @@ def _parse_config(text: str):
     vals = {}
     for part in text.replace(",", "/").split("/"):
         part = part.strip()
-        if part in ("nnz", "rows"):  # what a tile holds (merge-path windows or rows)
+        if part in ("nnz", "rows", "hybrid"):  # what a tile holds (see Config.balance)
             vals["balance"] = part
             continue
         for key, name in (("TPR", "threads_per_row"), ("T", "tile_size"), ("U", "unroll"),
@@ -177,7 +177,7 @@ def main(argv=None) -> int:
     ap.add_argument("--case", default="c1")
     ap.add_argument("--config", default=None,
                     help="schedule override, e.g. T128/TPR8/U2/V1/B256 (append /nnz for "
-                         "merge-path windows)")
+                         "merge-path windows, /hybrid for long-row workgroups)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="bound on the CPU baseline's timed calls")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")

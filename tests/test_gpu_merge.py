@@ -1,9 +1,12 @@
-"""GPU parity of the merge-path (balance "nnz") SpMV and fused_spmv_axpy.
+"""GPU parity of the merge-path (balance "nnz") and hybrid (balance
+"hybrid") SpMV and fused_spmv_axpy.
 
 Each workgroup takes an equal share of rows plus nonzeros, finds its first and
 last rows with a search of the row pointers, sums the rows that begin in its
 share whole, and adds its piece of any row longer than a share to the scratch
-the last piece reads back.  The matrices put that logic at its edges: no
+the last piece reads back.  Hybrid tiles keep row tiles but leave rows longer
+than half a nonzero range to workgroups that each take one range, with the
+same piece combine.  The matrices put that logic at its edges: no
 nonzeros, one row, rows ending exactly at the last nonzero, a row spanning
 hundreds of windows (more than one wave of pieces to combine), long first and
 last rows, mostly empty rows, power-law and dense-row patterns, and more
@@ -24,7 +27,7 @@ from tests.util import csr, ragged, rel_inf
 from tilegen_amd import codegen as cg
 from tilegen_amd.codegen import Config
 from tilegen_amd.matrices import make_baseline
-from tilegen_amd.schedules import MERGE_TEST_SCHEDULES, schedule_id
+from tilegen_amd.schedules import HYBRID_TEST_SCHEDULES, MERGE_TEST_SCHEDULES, schedule_id
 from tilegen_amd.variant import Variant
 
 pytestmark = pytest.mark.gpu
@@ -54,8 +57,8 @@ def _again_onto_nan(kernel, cfg, A, first):
     assert np.array_equal(out, first)
 
 
-@pytest.mark.parametrize("cfg", MERGE_TEST_SCHEDULES,
-                         ids=[schedule_id(c) for c in MERGE_TEST_SCHEDULES])
+@pytest.mark.parametrize("cfg", MERGE_TEST_SCHEDULES + HYBRID_TEST_SCHEDULES,
+                         ids=[schedule_id(c) for c in MERGE_TEST_SCHEDULES + HYBRID_TEST_SCHEDULES])
 @pytest.mark.parametrize("kernel", ["spmv", "fused_spmv_axpy"])
 def test_merge_path_matches_oracle(kernel, cfg, hip_ready):
     for label, A in _cases().items():
@@ -94,6 +97,7 @@ def test_merge_path_agrees_with_row_tiles(hip_ready):
         T, tpr, U, B = base
         rows = Variant("spmv", Config(tile_size=T, threads_per_row=tpr, unroll=U,
                                       block_size=B)).run(A, **ops)
-        merge = Variant("spmv", Config(tile_size=T, threads_per_row=tpr, unroll=U,
-                                       block_size=B, balance="nnz")).run(A, **ops)
-        assert rel_inf(merge, rows) <= TOL, case_id
+        for balance in ("nnz", "hybrid"):
+            other = Variant("spmv", Config(tile_size=T, threads_per_row=tpr, unroll=U,
+                                           block_size=B, balance=balance)).run(A, **ops)
+            assert rel_inf(other, rows) <= TOL, (case_id, balance)

@@ -205,7 +205,7 @@ def test_merge_source_and_refusals():
     cfg = Config(tile_size=64, threads_per_row=8, unroll=2, block_size=512, balance="nnz")
     for k in ("spmv", "fused_spmv_axpy"):
         g = cg.generate(ks[k], cfg, backend="hip", write=False)
-        assert "tg_mp_search(indptr, row_lim, t0, X)" in g.source
+        assert "tg_mp_search(indptr, row_lim, t0, X, 1)" in g.source
         assert "tg_mp_commit(wdx, wf, wl, t, &tot)" in g.source
         tiling = [e for e in cg._passes.run_pipeline(ks[k], cfg, backend="hip").pass_log
                   if e["pass"] == "tiling"][0]
@@ -223,3 +223,116 @@ def test_merge_source_and_refusals():
     # the CPU backend ignores it (like threads_per_row and block_size)
     cpu = cg.generate(ks["spmv"], cfg, backend="cpu", write=False)
     assert "tg_mp_" not in cpu.source
+
+
+# --------------------------------------------------------------------------- #
+# hybrid tiles: row tiles plus long-row workgroups over equal nonzero ranges
+# --------------------------------------------------------------------------- #
+def hybrid_pieces(indptr, M: int, CH: int, cap: int = cg.MERGE_CAP):
+    """The long-row workgroups as the emitter writes them: for every range e,
+    the (row, begin, end, ef, el, e, cut) pieces it sums, and the number of
+    rows it listed."""
+    nnz = int(indptr[M])
+    LH = CH // 2
+    GL = -(-nnz // CH) if nnz > 0 else 0
+    out, listed = [], []
+    for e in range(GL):
+        p0, p1 = e * CH, min(e * CH + CH, nnz)
+        ra = max(0, _search0(indptr, M, p0 + 1, nnz) - 1)  # the row holding nonzero p0
+        rows = []
+        r = ra
+        while r < M and int(indptr[r]) < p1:
+            rs, re = int(indptr[r]), int(indptr[r + 1])
+            if re - rs > LH and re > p0:
+                rows.append(r)
+            r += 1
+        listed.append(len(rows))
+        for row in rows:
+            rs, re = int(indptr[row]), int(indptr[row + 1])
+            ef, el = rs // CH, (re - 1) // CH
+            cut = el > ef and el < cap
+            if not cut and ef != e:
+                continue
+            q0 = max(p0, rs) if cut else rs
+            q1 = min(p1, re) if cut else re
+            out.append((row, q0, q1, ef, el, e, cut))
+    return out, listed
+
+
+def _search0(indptr, R, t, nnz):
+    """``tg_mp_search`` with row weight 0 (nonzero positions)."""
+    g = int(float(t) * (float(R) / float(nnz))) if nnz > 0 else 0
+    qs = [g - 24 + l if l < 48 else
+          (g + 24 + (32 << (2 * ((l - 48) >> 1))) if l & 1 else
+           g - 24 - (32 << (2 * ((l - 48) >> 1)))) for l in range(64)]
+    lo, hi = 0, R
+    while True:
+        qs = [min(max(q, lo), hi) for q in qs]
+        ge = [int(indptr[q]) >= t for q in qs]
+        a = max([lo - 1] + [q for q, g_ in zip(qs, ge) if not g_])
+        b = min([hi] + [q for q, g_ in zip(qs, ge) if g_])
+        lo, hi = a + 1, b
+        if lo >= hi:
+            return hi
+        s = (hi - lo + 62) // 63
+        qs = [lo + l * s for l in range(64)]
+
+
+@pytest.mark.parametrize("CH", [128, 512, 2048, 4096])
+def test_hybrid_long_rows_summed_once(CH):
+    """Every row longer than CH / 2 is summed exactly once by the long-row
+    workgroups (whole by one range, or as pieces that tile it, one per range
+    from its first to its last), no range lists more than 3 such rows (the
+    kernel's list holds 8), and no range holds two pieces of one kind."""
+    LH = CH // 2
+    for label, A in _cases():
+        M = A.shape[0]
+        pieces, listed = hybrid_pieces(A.indptr, M, CH)
+        assert max(listed, default=0) <= 3, (label, max(listed))
+        lens = np.diff(A.indptr)
+        by_row = {}
+        for p in pieces:
+            by_row.setdefault(p[0], []).append(p)
+        assert set(by_row) == set(np.nonzero(lens > LH)[0].tolist()), label
+        for row, ps in by_row.items():
+            rs, re = int(A.indptr[row]), int(A.indptr[row + 1])
+            if len(ps) == 1 and not ps[0][6]:
+                assert (ps[0][1], ps[0][2]) == (rs, re)
+                continue
+            ps.sort(key=lambda p: p[5])
+            ef, el = ps[0][3], ps[0][4]
+            assert [p[5] for p in ps] == list(range(ef, el + 1)), (label, row)
+            assert ps[0][1] == rs and ps[-1][2] == re
+            assert all(a[2] == b[1] for a, b in zip(ps, ps[1:]))
+        kinds = {}
+        for p in pieces:
+            if p[6]:
+                k = (p[5], p[5] == p[3])
+                assert k not in kinds, (label, k)
+                kinds[k] = p[0]
+
+
+def test_hybrid_source_and_geometry():
+    from tilegen_amd import dsl
+    ks = dsl.standard_kernels()
+    cfg = Config(tile_size=64, threads_per_row=8, unroll=2, block_size=512, balance="hybrid")
+    g = cg.generate(ks["spmv"], cfg, backend="hip", write=False)
+    assert "tg_mp_search(indptr, row_end, p0 + 1, nnz, 0)" in g.source
+    assert "(nnz + 2048 - 1) / 2048" in g.host_source
+    assert g.geometry.grid(100000, 794591) == 1563 + 388
+    assert g.geometry.grid(0, 5) == 0 and g.geometry.grid(10, 0) == 1
+    assert cfg.short().endswith("/hybrid")
+
+
+def test_hybrid_rows_past_the_scratch_stay_whole():
+    """With a scratch of 4 ranges, a long row reaching range 4 or later is summed
+    whole by its first range and by no other; one within the first 4 is cut."""
+    A = ragged(12, 300, 4000, 3, long_rows=[(2, 300), (250, 900)])
+    pieces, _ = hybrid_pieces(A.indptr, 300, 128, cap=4)
+    by_row = {}
+    for p in pieces:
+        by_row.setdefault(p[0], []).append(p)
+    assert len(by_row[2]) > 1 and all(p[6] for p in by_row[2])
+    assert len(by_row[250]) == 1 and not by_row[250][0][6]
+    rs, re = int(A.indptr[250]), int(A.indptr[251])
+    assert by_row[250][0][1:3] == (rs, re) and by_row[250][0][5] == rs // 128

@@ -61,7 +61,8 @@ BASELINE = Config(tile_size=32, threads_per_row=1, unroll=1, vector_width=1, blo
 
 _WAVE = 64
 _LDS_LIMIT = 64 * 1024
-# kernels whose schedules also come with merge-path windows (Config.balance)
+# kernels whose schedules also come with merge-path windows and hybrid tiles
+# (Config.balance)
 MERGE_KERNELS = ("spmv", "fused_spmv_axpy")
 ROTATE_BYTES = 640 << 20
 
@@ -163,8 +164,10 @@ def enumerate_configs(kernel: Optional[str] = None, K: int = 8
         reason = illegal_reason(cfg) if kernel is None else illegal_reason_for(kernel, cfg, K)
         out.append((cfg, reason))
     if kernel in MERGE_KERNELS:
-        # the same schedules with merge-path windows instead of row tiles
-        out += [(dataclasses.replace(c, balance="nnz"), r) for c, r in list(out)]
+        # the same schedules with merge-path windows and with hybrid tiles
+        rows = list(out)
+        for balance in ("nnz", "hybrid"):
+            out += [(dataclasses.replace(c, balance=balance), r) for c, r in rows]
     return out
 
 
@@ -333,7 +336,7 @@ def _candidate_configs(kernel: str, K: int, budget: int, mode: str, rng: random.
         best = out[0]
         steps = [(key, value) for key in SEARCH_SPACE for value in SEARCH_SPACE[key]]
         if kernel in MERGE_KERNELS:
-            steps.append(("balance", "nnz"))
+            steps += [("balance", "nnz"), ("balance", "hybrid")]
         for key, value in steps:
             add(Config(**{**best.to_dict(), key: value}))
             if len(out) >= budget:

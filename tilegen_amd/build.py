@@ -89,7 +89,8 @@ def warm_cache(verbose: bool = False) -> int:
     from .dsl import standard_kernels
     from .matrices import baseline_case
     from .passes import PASS_NAMES
-    from .schedules import MERGE_TEST_SCHEDULES, TEST_KERNELS, TEST_SCHEDULES, TUNED
+    from .schedules import (HYBRID_TEST_SCHEDULES, MERGE_TEST_SCHEDULES, TEST_KERNELS,
+                            TEST_SCHEDULES, TUNED)
     from .verify import compile_generated
 
     kernels = standard_kernels()
@@ -102,7 +103,7 @@ def warm_cache(verbose: bool = False) -> int:
         todo.append((name, Config(tile_size=32, threads_per_row=4, unroll=2, vector_width=1,
                                   block_size=256, inject_bug=True), ()))
     for name in ("spmv", "fused_spmv_axpy"):
-        for cfg in MERGE_TEST_SCHEDULES:
+        for cfg in MERGE_TEST_SCHEDULES + HYBRID_TEST_SCHEDULES:
             todo.append((name, cfg, ()))
     for name, cases in DEFAULT_CASES.items():
         for case_id in cases:

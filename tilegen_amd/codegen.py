@@ -89,9 +89,11 @@ class Config:
 
     tile_size T (rows per workgroup), threads_per_row TPR, unroll U,
     vector_width V, block_size B (lanes per workgroup).  ``balance`` is what
-    a tile holds on the HIP backend: ``"rows"`` (T consecutive rows) or
-    ``"nnz"`` (an equal share of rows plus nonzeros, about T rows' worth, for
-    SpMV-shaped kernels; see ``_hip_scalar_reduce``).  It has no counterpart in
+    a tile holds on the HIP backend: ``"rows"`` (T consecutive rows),
+    ``"nnz"`` (an equal share of rows plus nonzeros, about T rows' worth) or
+    ``"hybrid"`` (T rows, with rows past a length threshold left to extra
+    workgroups that each take an equal range of nonzeros); the last two are for
+    SpMV-shaped kernels (see ``_hip_scalar_reduce``).  It has no counterpart in
     the reference and is left out of ``to_dict``/``hash`` at its default, so
     every reference schedule keeps its name.
     """
@@ -128,7 +130,7 @@ class Config:
     def short(self) -> str:
         return "T%d/TPR%d/U%d/V%d/B%d%s" % (self.tile_size, self.threads_per_row,
                                             self.unroll, self.vector_width, self.block_size,
-                                            "/nnz" if self.balance == "nnz" else "")
+                                            {"rows": ""}.get(self.balance, "/" + self.balance))
 
 
 @dataclass
@@ -177,19 +179,30 @@ def _lowering(kernel: Kernel) -> Lowering:
 
 @dataclass
 class LaunchGeometry:
-    """Grid rule of a HIP variant: ``grid = ceil(rows / rows_per_block)``."""
+    """Grid rule of a HIP variant: ``grid = ceil(rows / rows_per_block)``,
+    plus ``ceil(nnz / nnz_chunk)`` workgroups ahead of those when
+    ``nnz_chunk`` is set (hybrid tiles' long-row workgroups)."""
 
     rows_per_block: int
     block: int
     lds_bytes: int
     rows_symbol: str = "M"
+    nnz_chunk: int = 0
 
-    def grid(self, rows: int) -> int:
-        return (int(rows) + self.rows_per_block - 1) // self.rows_per_block if rows > 0 else 0
+    def grid(self, rows: int, nnz: int = 0) -> int:
+        if rows <= 0:
+            return 0
+        g = (int(rows) + self.rows_per_block - 1) // self.rows_per_block
+        if self.nnz_chunk and nnz > 0:
+            g += (int(nnz) + self.nnz_chunk - 1) // self.nnz_chunk
+        return g
 
     def to_dict(self) -> Dict[str, Any]:
-        return {"rows_per_block": self.rows_per_block, "block": self.block,
-                "lds_bytes": self.lds_bytes, "rows_symbol": self.rows_symbol}
+        d = {"rows_per_block": self.rows_per_block, "block": self.block,
+             "lds_bytes": self.lds_bytes, "rows_symbol": self.rows_symbol}
+        if self.nnz_chunk:
+            d["nnz_chunk"] = self.nnz_chunk
+        return d
 
 
 @dataclass
@@ -693,7 +706,15 @@ def launch_geometry(plan: Plan, low: Lowering) -> LaunchGeometry:
         return LaunchGeometry(low.tile if low.tiled else slots, B, 0, plan.row_extent)
     rows = low.tile if low.tiled else slots
     lds = 8 * (rows + 1) if (plan.kind == "scalar_reduce" and low.tiled) else 0
-    return LaunchGeometry(rows, B, lds, plan.row_extent)
+    chunk = hybrid_chunk(low) if (plan.kind == "scalar_reduce" and low.tiled
+                                  and low.balance == "hybrid") else 0
+    return LaunchGeometry(rows, B, lds, plan.row_extent, chunk)
+
+
+def hybrid_chunk(low: Lowering) -> int:
+    """Nonzeros per long-row workgroup of hybrid tiles: two passes of the whole
+    workgroup; rows longer than half of it are summed by those workgroups."""
+    return 2 * min(low.block_size, 1024) * max(1, low.unroll)
 
 
 def _check_hip_schedule(plan: Plan, low: Lowering) -> None:
@@ -709,9 +730,10 @@ def _check_hip_schedule(plan: Plan, low: Lowering) -> None:
         raise ValueError("unroll must be in 1..16, got %d" % low.unroll)
     if low.tiled and low.tile > 4096:
         raise ValueError("tile_size %d exceeds 4096 rows per workgroup" % low.tile)
-    if low.balance == "nnz" and not (low.tiled and plan.kind == "scalar_reduce"):
-        raise ValueError("balance 'nnz' needs a tiled kernel that reduces over each row "
-                         "(SpMV-shaped); %s %s" % (plan.kind, "untiled" if not low.tiled else ""))
+    if low.balance != "rows" and not (low.tiled and plan.kind == "scalar_reduce"):
+        raise ValueError("balance '%s' needs a tiled kernel that reduces over each row "
+                         "(SpMV-shaped); %s %s" % (low.balance, plan.kind,
+                                                   "untiled" if not low.tiled else ""))
 
 
 def _long_row_test(length: str, long_: int, huge: int) -> str:
@@ -750,12 +772,14 @@ def _merge_decls(pre: _W) -> None:
 // nonzeros, then one item that ends it); the launch's items are cut into one
 // window per workgroup.
 //
-// Smallest r in [0, R] with r + indptr[r] >= t (R when there is none).  Run by
+// Smallest r in [0, R] with wt * r + indptr[r] >= t (R when there is none), for
+// wt 1 (merge-path items) or 0 (nonzero positions); X = wt * R + nnz.  Run by
 // all 64 lanes of one wave, one row pointer per lane per round.  The first round
 // probes 48 consecutive rows around the proportional guess and 16 rows at
 // growing distances either side of it; each later round probes 64 evenly spaced
 // rows of the bracket left, so the bracket shrinks at least 63-fold per round.
-__device__ tg_i64 tg_mp_search(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 t, tg_i64 X) {
+__device__ tg_i64 tg_mp_search(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 t, tg_i64 X,
+                               int wt) {
   const int l = threadIdx.x & 63;
   const tg_i64 g = X > 0 ? (tg_i64)((double)t * ((double)R / (double)X)) : 0;
   tg_i64 q;
@@ -769,7 +793,7 @@ __device__ tg_i64 tg_mp_search(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i
   #pragma unroll 1
   for (;;) {
     q = q < lo ? lo : (q > hi ? hi : q);
-    const bool ge = q + indptr[q] >= t;
+    const bool ge = (wt ? q : 0) + indptr[q] >= t;
     tg_i64 a = ge ? lo - 1 : q;   // rows known to start before t
     tg_i64 b = ge ? q : hi;       // rows known to start at or after t
     #pragma unroll
@@ -847,14 +871,14 @@ def _merge_window(w: _W, TR: int, WAVES: int) -> None:
     w("const tg_i64 t1 = t0 + D < X ? t0 + D : X;")
     w("// first and last rows: the first row beginning at or after t0 (t1)")
     w.open("if (threadIdx.x < 64)")
-    w("const tg_i64 a = wdx == 0 ? 0 : tg_mp_search(indptr, row_lim, t0, X);")
+    w("const tg_i64 a = wdx == 0 ? 0 : tg_mp_search(indptr, row_lim, t0, X, 1);")
     w("if (threadIdx.x == 0) s_win[0] = a;")
     w("if (threadIdx.x < 2) s_win[2 + threadIdx.x] = a - 1 + (tg_i64)threadIdx.x >= 0 ? "
       "indptr[a - 1 + threadIdx.x] : 0;")
     w.close()
     sel = "threadIdx.x >= 64 && threadIdx.x < 128" if WAVES > 1 else "threadIdx.x < 64"
     w.open("if (%s)" % sel)
-    w("const tg_i64 b = wdx == G - 1 ? row_lim : tg_mp_search(indptr, row_lim, t1, X);")
+    w("const tg_i64 b = wdx == G - 1 ? row_lim : tg_mp_search(indptr, row_lim, t1, X, 1);")
     w("const int l = threadIdx.x & 63;")
     w("if (l == 0) s_win[1] = b;")
     w("if (l < 2) s_win[4 + l] = b - 1 + l >= 0 ? indptr[b - 1 + l] : 0;")
@@ -869,6 +893,89 @@ def _merge_window(w: _W, TR: int, WAVES: int) -> None:
     w("const bool pc_out = r1 > r0 && s_win[5] - s_win[4] > D && "
       "(r1 - 1 + s_win[5] - 1) / D < %d;" % MERGE_CAP)
     w("const tg_i64 r_own = pc_out ? r1 - 1 : r1;  // rows summed whole, %d at a time" % TR)
+
+
+def _hybrid_ranges(w: _W, plan: Plan, step, out_name: str, B: int, U: int, ALIGN: int,
+                   WAVES: int, CH: int, LH: int) -> None:
+    """The long-row workgroups of hybrid tiles (defines GL; those workgroups
+    return).  Workgroup e < GL takes nonzeros [e CH, (e+1) CH): it finds the
+    row holding the first of them with ``tg_mp_search``, lists the rows from
+    there on that are longer than LH and meet the range, and sums each one's
+    part in the range with the whole workgroup.  A row within one range is
+    written directly; a row spanning ranges is combined by ``tg_mp_commit``
+    (its pieces in range order), or, when its last range has no scratch slot,
+    summed whole by its first range."""
+    row = plan.row_idx.name
+    w("// workgroups below GL sum the rows longer than %d nonzeros, %d nonzeros each;" % (LH, CH))
+    w("// the rest are row tiles, which leave those rows alone")
+    w("const tg_i64 GL = nnz > 0 ? (nnz + %d) / %d : 0;" % (CH - 1, CH))
+    w.open("if ((tg_i64)blockIdx.x < GL)")
+    w("__shared__ tg_i64 s_ra;")
+    w("__shared__ tg_i64 s_lr[8];  // long rows meeting the range (at most 3)")
+    w("__shared__ int s_nl;")
+    w("__shared__ double s_hred[%d];" % WAVES)
+    w("const tg_i64 e = blockIdx.x;")
+    w("const tg_i64 p0 = e * %d, p1 = p0 + %d < nnz ? p0 + %d : nnz;" % (CH, CH, CH))
+    w("// the row holding nonzero p0: one before the first row that begins past it")
+    w.open("if (threadIdx.x < 64)")
+    w("const tg_i64 a = tg_mp_search(indptr, row_end, p0 + 1, nnz, 0) - 1;")
+    w("if (threadIdx.x == 0) { s_ra = a < 0 ? 0 : a; s_nl = 0; }")
+    w.close()
+    w("__syncthreads();")
+    w("const tg_i64 ra = s_ra;")
+    w("// rows from ra on, up to the first that begins at or past p1")
+    w("#pragma unroll 1")
+    w.open("for (tg_i64 base = ra; ; base += %d)" % B)
+    w("const tg_i64 r = base + (tg_i64)threadIdx.x;")
+    w("bool past = true;")
+    w.open("if (r < row_end)")
+    w("const tg_i64 rs = indptr[r];")
+    w("past = rs >= p1;")
+    w.open("if (!past)")
+    w("const tg_i64 re = indptr[r + 1];")
+    w.open("if (re - rs > %d && re > p0)" % LH)
+    w("const int k = atomicAdd(&s_nl, 1);")
+    w("if (k < 8) s_lr[k] = r;")
+    w.close()
+    w.close()
+    w.close()
+    w("if (__syncthreads_or(past)) break;")
+    w.close()
+    w("const int nl = s_nl < 8 ? s_nl : 8;")
+    w("#pragma unroll 1")
+    w.open("for (int k = 0; k < nl; ++k)")
+    w("const tg_i64 row = s_lr[k];")
+    w("const tg_i64 rs = indptr[row], re = indptr[row + 1];")
+    w("const tg_i64 ef = rs / %d, el = (re - 1) / %d;  // the ranges its nonzeros lie in"
+      % (CH, CH))
+    w("const bool cut = el > ef && el < %d;" % MERGE_CAP)
+    w("if (!cut && ef != e) continue;  // kept whole: summed by its first range only")
+    w("const tg_i64 q0 = cut && p0 > rs ? p0 : rs, q1 = cut && p1 < re ? p1 : re;")
+    w("double cacc = 0.0;")
+    w("#pragma unroll 1")
+    w.open("for (tg_i64 q = (q0 & ~(tg_i64)%d) + (tg_i64)threadIdx.x * %d; q < q1; q += %d)"
+           % (ALIGN - 1, U, B * U))
+    step("q", "q0", "q1", "cacc")
+    w.close()
+    w("cacc = tg_segsum<64>(cacc);")
+    w("if ((threadIdx.x & 63) == 0) s_hred[threadIdx.x >> 6] = cacc;")
+    w("__syncthreads();")
+    w.open("if (threadIdx.x < 64)")
+    w("double t = 0.0;")
+    w("#pragma unroll")
+    w("for (int v = 0; v < %d; ++v) t += s_hred[v];" % WAVES)
+    w("double tot = t;")
+    w("const bool done = !cut || tg_mp_commit(e, ef, el, t, &tot);")
+    w.open("if (done && threadIdx.x == 0)")
+    env = _Env({row: "row"}, acc="tot")
+    w("__builtin_nontemporal_store(%s, %s + %s);" % (
+        _cexpr(plan.final_expr, env), out_name, _offset(plan.out_tensor, plan.out.indices, env)))
+    w.close()
+    w.close()
+    w("__syncthreads();")
+    w.close()
+    w("return;")
+    w.close()
 
 
 def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeometry,
@@ -910,20 +1017,63 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     if wave_tier:
         MED = 2 * STEP
         WLONG = 4 * WAVE * U
+    row = plan.row_idx.name
+    col = plan.col_idx.name
+    gathered = _gather_operand(plan)
+
+    def step(q: str, lo: str, hi: str, acc: str) -> None:
+        """Load U consecutive nonzeros at q (masked to [lo, hi)), gather, FMA."""
+        w("tg_i64 ci[%d]; double cv[%d];" % (U, U))
+        if U % 2 == 0:
+            w.open("if (pair_ok && %s + %d <= nnz)" % (q, U))
+            for u in range(0, U, 2):
+                w("{ const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + %s + %d));"
+                  " ci[%d] = a.x; ci[%d] = a.y; }" % (q, u, u, u + 1))
+                w("{ const tg_f64x2 b = __builtin_nontemporal_load((const tg_f64x2*)(data + %s + %d));"
+                  " cv[%d] = b.x; cv[%d] = b.y; }" % (q, u, u, u + 1))
+            w.close()
+            w.open("else")
+        else:
+            w.open("")
+        for u in range(U):
+            w("ci[%d] = %s + %d < nnz ? __builtin_nontemporal_load(indices + %s + %d) : 0;"
+              % (u, q, u, q, u))
+            w("cv[%d] = %s + %d < nnz ? __builtin_nontemporal_load(data + %s + %d) : 0.0;"
+              % (u, q, u, q, u))
+        w.close()
+        w("double xv[%d];" % U)
+        w("#pragma unroll")
+        w.open("for (int u = 0; u < %d; ++u)" % U)
+        w("const tg_i64 pu = %s + u;" % q)
+        w("const bool in_row = pu >= %s && pu < %s;" % (lo, hi))
+        w("cv[u] = in_row ? cv[u] : 0.0;")
+        w("ci[u] = in_row ? ci[u] : 0;")
+        w("xv[u] = %s;" % _cexpr(gathered, _Env({row: "row", col: "ci[u]"}, p="pu")))
+        w.close()
+        w("#pragma unroll")
+        w.open("for (int u = 0; u < %d; ++u)" % U)
+        w("%s += %s;" % (acc, _value_with(plan, "cv[u]", "xv[u]", row, "ci[u]")))
+        w.close()
+
     merge = coop and low.balance == "nnz"
-    if merge:
+    hybrid = coop and low.balance == "hybrid"
+    if merge or hybrid:
         if pre is None:
-            raise ValueError("merge-path tiles need file-scope declarations")
+            raise ValueError("merge-path and hybrid tiles need file-scope declarations")
         _merge_decls(pre)
+    if merge:
         # a window holds about T rows' worth of items but may hold several times
         # T short rows; a batch is at least one row per lane group
         TR = max(TR, SLOTS)
         R = (TR + SLOTS - 1) // SLOTS
-    row = plan.row_idx.name
-    col = plan.col_idx.name
+    if hybrid:
+        CH = hybrid_chunk(low)
+        LH = CH // 2  # at most 3 rows this long meet one range of CH nonzeros
 
     if merge:
         w("const tg_i64 row_lim = %s;  // rows this launch writes" % bound)
+    elif hybrid:
+        w("const tg_i64 row_end = %s;" % bound)
     else:
         w("const tg_i64 row_end = %s;" % bound)
         w("const tg_i64 row0 = (tg_i64)blockIdx.x * %d;" % TR)
@@ -934,6 +1084,9 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("// sub-buffer may be only 8-byte aligned, which takes the per-element loads")
         w("const bool pair_ok = ((((unsigned long long)indices) | "
           "((unsigned long long)data)) & 15) == 0;")
+    if hybrid:
+        _hybrid_ranges(w, plan, step, out_name, B, U, ALIGN, WAVES, CH, LH)
+        w("const tg_i64 row0 = ((tg_i64)blockIdx.x - GL) * %d;" % TR)
     if low.tiled:
         w("// row pointers of this tile, staged once in LDS")
         w("__shared__ tg_i64 s_ptr[%d];" % (TR + 1))
@@ -974,59 +1127,31 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("rs[r] = live ? indptr[ri] : 0;")
         w("re[r] = live ? indptr[ri + 1] : 0;")
     if coop:
+        skip = ""
+        if hybrid:
+            w("const bool lw = re[r] - rs[r] > %d;  // summed by the long-row workgroups" % LH)
+            skip = "lw || "
         if wave_tier:
             w("const tg_i64 len = re[r] - rs[r];")
-            w("coop[r] = len > %d && (len * t_rows > 2 * t_nnz || len > %d);" % (MED, LONG))
+            w("coop[r] = %slen > %d && (len * t_rows > 2 * t_nnz || len > %d);"
+              % (skip, MED, LONG) if not hybrid else
+              "coop[r] = lw || (len > %d && (len * t_rows > 2 * t_nnz || len > %d));"
+              % (MED, LONG))
         else:
-            w("coop[r] = re[r] - rs[r] > %d;" % LONG)
+            w("coop[r] = %sre[r] - rs[r] > %d;" % (skip, LONG))
         w.open("if (coop[r])")
+        listed = "lane == 0 && !lw" if hybrid else "lane == 0"
         if wave_tier:
-            w.open("if (lane == 0)")
+            w.open("if (%s)" % listed)
             w("if (re[r] - rs[r] > %d) s_long[atomicAdd(&s_nlong, 1)] = lr;" % WLONG)
             w("else s_med[atomicAdd(&s_nmed, 1)] = lr;")
             w.close()
         else:
-            w("if (lane == 0) s_long[atomicAdd(&s_nlong, 1)] = lr;")
+            w("if (%s) s_long[atomicAdd(&s_nlong, 1)] = lr;" % listed)
         w("re[r] = rs[r];  // the lane group skips it")
         w.close()
     w("acc[r] = 0.0;")
     w.close()
-
-    gathered = _gather_operand(plan)
-
-    def step(q: str, lo: str, hi: str, acc: str) -> None:
-        """Load U consecutive nonzeros at q (masked to [lo, hi)), gather, FMA."""
-        w("tg_i64 ci[%d]; double cv[%d];" % (U, U))
-        if U % 2 == 0:
-            w.open("if (pair_ok && %s + %d <= nnz)" % (q, U))
-            for u in range(0, U, 2):
-                w("{ const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + %s + %d));"
-                  " ci[%d] = a.x; ci[%d] = a.y; }" % (q, u, u, u + 1))
-                w("{ const tg_f64x2 b = __builtin_nontemporal_load((const tg_f64x2*)(data + %s + %d));"
-                  " cv[%d] = b.x; cv[%d] = b.y; }" % (q, u, u, u + 1))
-            w.close()
-            w.open("else")
-        else:
-            w.open("")
-        for u in range(U):
-            w("ci[%d] = %s + %d < nnz ? __builtin_nontemporal_load(indices + %s + %d) : 0;"
-              % (u, q, u, q, u))
-            w("cv[%d] = %s + %d < nnz ? __builtin_nontemporal_load(data + %s + %d) : 0.0;"
-              % (u, q, u, q, u))
-        w.close()
-        w("double xv[%d];" % U)
-        w("#pragma unroll")
-        w.open("for (int u = 0; u < %d; ++u)" % U)
-        w("const tg_i64 pu = %s + u;" % q)
-        w("const bool in_row = pu >= %s && pu < %s;" % (lo, hi))
-        w("cv[u] = in_row ? cv[u] : 0.0;")
-        w("ci[u] = in_row ? ci[u] : 0;")
-        w("xv[u] = %s;" % _cexpr(gathered, _Env({row: "row", col: "ci[u]"}, p="pu")))
-        w.close()
-        w("#pragma unroll")
-        w.open("for (int u = 0; u < %d; ++u)" % U)
-        w("%s += %s;" % (acc, _value_with(plan, "cv[u]", "xv[u]", row, "ci[u]")))
-        w.close()
 
     w("// first step of every row in flight before any accumulation")
     w("#pragma unroll")
@@ -1674,15 +1799,17 @@ def _hip_kernel_text(kernel: Kernel, config: Config, plan: Plan, low: Lowering,
 def emit_hip(kernel: Kernel, config: Config) -> str:
     """Device translation unit of a lowered kernel (hipRTC input)."""
     plan, low = _plan(kernel), _lowering(kernel)
-    if config.balance == "nnz" and not low.tiled:
-        raise ValueError("balance 'nnz' needs a tile (tile_size > 1); %s is untiled"
-                         % config.short())
+    if config.balance != "rows" and config.tile_size <= 1:
+        raise ValueError("balance '%s' needs a tile (tile_size > 1); %s is untiled"
+                         % (config.balance, config.short()))
     _check_hip_schedule(plan, low)
     _sig, args, _info = abi_of(kernel)
     geo = launch_geometry(plan, low)
     extra = ["target      : %s (wave%d)" % (HIP_ARCH, WAVE),
-             "launch      : grid = ceil(%s / %d), block = %d, lds = %d B"
-             % (geo.rows_symbol, geo.rows_per_block, geo.block, geo.lds_bytes)]
+             "launch      : grid = ceil(%s / %d)%s, block = %d, lds = %d B"
+             % (geo.rows_symbol, geo.rows_per_block,
+                " + ceil(nnz / %d)" % geo.nnz_chunk if geo.nnz_chunk else "",
+                geo.block, geo.lds_bytes)]
     return "\n".join([_header(kernel, config, "hip", low, extra), _HIP_PRELUDE.strip(), "",
                       _hip_kernel_text(kernel, config, plan, low, args, geo), ""])
 
@@ -1716,7 +1843,7 @@ def emit_hip_host(kernel: Kernel, config: Config) -> str:
     nnz = "nnz" if "nnz" in dims else "0"
     params = ", ".join("%s %s" % a for a in args)
     text = """/* TileGen HIP launcher for %(sym)s -- generated, DO NOT EDIT.
- * schedule %(sched)s; grid = ceil(%(rows)s / %(rpb)d), block = %(block)d, lds = %(lds)d B */
+ * schedule %(sched)s; grid = ceil(%(rows)s / %(rpb)d)%(extra_grid)s, block = %(block)d, lds = %(lds)d B */
 #include <stdint.h>
 #include <string.h>
 #include "tgrt.h"
@@ -1741,7 +1868,7 @@ int tgv_geometry(int64_t M, int64_t N, int64_t K, int64_t nnz,
                  int64_t* grid, int32_t* block, int32_t* lds) {
   (void)N; (void)K; (void)nnz;
   const int64_t rows = %(rows_expr)s;
-  *grid = rows > 0 ? (rows + %(rpb)d - 1) / %(rpb)d : 0;
+  *grid = rows > 0 ? (rows + %(rpb)d - 1) / %(rpb)d : 0;%(extra)s
   *block = %(block)d;
   *lds = %(lds)d;
   return 0;
@@ -1773,6 +1900,10 @@ int tgv_launch_async(void* stream, %(params)s) {
         "rows_expr": rows if rows in dims else "M", "params": params,
         "pack": "\n".join(pack), "nargs": len(args), "names": ", ".join(names),
         "sig": sig, "M": "M" if "M" in dims else "0", "N": ndim, "K": kdim, "nnz": nnz,
+        "extra_grid": " + ceil(nnz / %d)" % geo.nnz_chunk if geo.nnz_chunk else "",
+        "extra": ("\n  /* long-row workgroups of hybrid tiles, ahead of the row tiles */"
+                  "\n  if (*grid > 0 && nnz > 0) *grid += (nnz + %d - 1) / %d;"
+                  % (geo.nnz_chunk, geo.nnz_chunk)) if geo.nnz_chunk else "",
     }
     return text
 

@@ -213,8 +213,10 @@ class Transform:
 class Tile(Transform):
     index: Index = None  # type: ignore[assignment]
     size: int = 0
-    #: what a tile holds: ``rows`` (``size`` consecutive rows) or ``nnz`` (an equal
+    #: what a tile holds: ``rows`` (``size`` consecutive rows), ``nnz`` (an equal
     #: share of rows plus nonzeros, about ``size`` rows' worth: merge-path windows)
+    #: or ``hybrid`` (``size`` rows, rows past a length threshold left to
+    #: workgroups that each take an equal range of nonzeros)
     by: str = "rows"
     kind: ClassVar[str] = "tile"
 
@@ -459,8 +461,8 @@ def _check_transform(t: Transform, known: set) -> None:
                              % (t.kind, ix.name))
     if isinstance(t, Tile) and t.size <= 0:
         raise ValueError("transform %r factor/size must be > 0" % t.kind)
-    if isinstance(t, Tile) and t.by not in ("rows", "nnz"):
-        raise ValueError("tile 'by' must be 'rows' or 'nnz', got %r" % t.by)
+    if isinstance(t, Tile) and t.by not in ("rows", "nnz", "hybrid"):
+        raise ValueError("tile 'by' must be 'rows', 'nnz' or 'hybrid', got %r" % t.by)
     if isinstance(t, Split) and t.factor <= 0:
         raise ValueError("transform %r factor/size must be > 0" % t.kind)
     if isinstance(t, Unroll) and t.factor <= 0:

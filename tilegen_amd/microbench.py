@@ -21,7 +21,7 @@ rowgather
     Infinity Cache) and from a 3.2 MB one, with one 512-byte row written per
     16 gathered, cold (table copies rotated) and warm.
 flat
-    A SpMV case's accesses without its rows (c1 and c2 by default): the
+    A SpMV case's accesses without its rows (every SpMV case by default): the
     matrix's own ``indices`` and ``data`` streamed with one 128-bit load of
     each per lane, ``x`` gathered at those indices, 8 lanes summing 16
     products and one double stored per 16, with no row pointers, LDS or
@@ -395,7 +395,7 @@ def main(argv=None) -> int:
     ap.add_argument("--out", default="results")
     ap.add_argument("--only", choices=["flat"], default=None,
                     help="run one probe and print its table (results/ is left as it is)")
-    ap.add_argument("--flat-cases", default="c1,c2",
+    ap.add_argument("--flat-cases", default="c1,c2,c3a,c3b",
                     help="SpMV cases the flat probe runs on (comma-separated)")
     a = ap.parse_args(argv)
     if rt.device_count() < 1:

@@ -177,6 +177,15 @@ def tiling(kernel: Kernel) -> Kernel:
         return kernel
     balance = getattr(getattr(kernel, "_config", None), "balance", "rows") or "rows"
     _set_transform(kernel, Tile, same, Tile(outer, size, balance))
+    if balance == "hybrid":
+        _log(kernel, "tiling",
+             "strip-mined '%s' into tiles of %d rows; rows longer than a long-row "
+             "workgroup's half share are summed by workgroups that each take an equal range "
+             "of nonzeros" % (outer.name, size),
+             "for %s in 0..extent" % outer.name,
+             "for nonzero range: long rows' pieces; for %s_o step %d: short %s_i: ..."
+             % (outer.name, size, outer.name))
+        return kernel
     if balance == "nnz":
         _log(kernel, "tiling",
              "split '%s' into windows of equal rows-plus-nonzeros (merge path), one per %d "

@@ -20,9 +20,13 @@ TUNED: Dict[str, Config] = {
     "c1": Config(tile_size=16, threads_per_row=8, unroll=2, vector_width=1, block_size=128),
     # 7 nonzeros per row: 4 lanes x 2
     "c2": Config(tile_size=128, threads_per_row=4, unroll=2, vector_width=1, block_size=256),
-    # skewed rows: short rows on 8/32-lane groups, rows over 8 group steps
-    # (128 / 512 nonzeros) taken by the whole workgroup
-    "c3a": Config(tile_size=64, threads_per_row=8, unroll=2, vector_width=1, block_size=512),
+    # skewed rows.  c3a: hybrid tiles, rows over 1024 nonzeros (half of a
+    # 2 x 256 x 4 range) summed by long-row workgroups over equal nonzero ranges,
+    # the rest on 4-lane groups (13.7 us against 17.4 with row tiles alone).
+    # c3b: row tiles, short rows on 32-lane groups, rows over 8 group steps (512
+    # nonzeros) taken by the whole workgroup (hybrid tiles tie at 10.4 us)
+    "c3a": Config(tile_size=64, threads_per_row=4, unroll=4, vector_width=1, block_size=256,
+                  balance="hybrid"),
     "c3b": Config(tile_size=32, threads_per_row=32, unroll=2, vector_width=1, block_size=1024),
     # K = 64: 16 lanes x 2 columns x 2 passes per row, 2 nonzeros' B rows in flight
     "c4": Config(tile_size=16, threads_per_row=16, unroll=2, vector_width=2, block_size=64),
@@ -65,8 +69,13 @@ MERGE_TEST_SCHEDULES: List[Config] = [
     Config(tile_size=8, threads_per_row=16, unroll=3, block_size=256, balance="nnz"),
 ]
 
+# The same for hybrid tiles (row tiles plus long-row workgroups over nonzero
+# ranges of 2 x block x unroll): ranges of 128 to 4096 nonzeros.
+HYBRID_TEST_SCHEDULES: List[Config] = [
+    Config(**{**c.to_dict(), "balance": "hybrid"}) for c in MERGE_TEST_SCHEDULES]
+
 
 def schedule_id(c: Config) -> str:
     return "T%d-TPR%d-U%d-V%d-B%d%s" % (c.tile_size, c.threads_per_row, c.unroll,
                                         c.vector_width, c.block_size,
-                                        "-nnz" if c.balance == "nnz" else "")
+                                        "" if c.balance == "rows" else "-" + c.balance)

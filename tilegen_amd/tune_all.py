@@ -19,6 +19,7 @@ import sys
 from typing import List, Optional, Sequence
 
 from .autotune import prune_log, tune, write_outputs
+from .codegen import Config
 from .env import probe
 from .matrices import build_corpus, corpus_classes
 
@@ -44,9 +45,8 @@ def run(matrix_dir: str, backend: str, kernels: Sequence[str] = ALL_KERNELS,
             out.append(res)
             w, m = res["winner"], res["winner_metrics"]
             if w:
-                log("%-16s %-16s winner T%d/TPR%d/U%d/V%d/B%d  median %.4f ms  %.2fx vs "
-                    "T32/TPR1/U1/V1/B128" % (cls, kernel, w["tile_size"], w["threads_per_row"],
-                                             w["unroll"], w["vector_width"], w["block_size"],
+                log("%-16s %-16s winner %s  median %.4f ms  %.2fx vs "
+                    "T32/TPR1/U1/V1/B128" % (cls, kernel, Config(**w).short(),
                                              m["ms_median"], m["speedup_vs_naive"] or 0.0))
             else:
                 log("%-16s %-16s no legal, verified variant" % (cls, kernel))
@@ -68,9 +68,8 @@ def render_markdown(results: List[dict], backend: str) -> str:
             lines.append("| %s | %s | none | | | | | |" % (r["matrix_class"], r["kernel"]))
             continue
         n = sum(1 for x in r["records"] if x.get("ms_min") is not None)
-        lines.append("| %s | %s | T%d/TPR%d/U%d/V%d/B%d | %.4f | %.1f | %.0f | %.2fx | %d |" % (
-            r["matrix_class"], r["kernel"], w["tile_size"], w["threads_per_row"], w["unroll"],
-            w["vector_width"], w["block_size"], m["ms_median"], m["gflops"],
+        lines.append("| %s | %s | %s | %.4f | %.1f | %.0f | %.2fx | %d |" % (
+            r["matrix_class"], r["kernel"], Config(**w).short(), m["ms_median"], m["gflops"],
             m["compulsory_gbs"], m["speedup_vs_naive"] or 0.0, n))
     return "\n".join(lines) + "\n"
 
