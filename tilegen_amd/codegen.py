@@ -951,10 +951,20 @@ def _hybrid_ranges(w: _W, plan: Plan, step, out_name: str, B: int, U: int, ALIGN
     w("const bool cut = el > ef && el < %d;" % MERGE_CAP)
     w("if (!cut && ef != e) continue;  // kept whole: summed by its first range only")
     w("const tg_i64 q0 = cut && p0 > rs ? p0 : rs, q1 = cut && p1 < re ? p1 : re;")
-    w("double cacc = 0.0;")
+    w("double cacc = 0.0, cacc2 = 0.0;")
+    w("// a piece spans at most two workgroup steps (plus one element of alignment):")
+    w("// both steps' loads go out together, the rest (whole rows) loops")
+    w("const tg_i64 qa = (q0 & ~(tg_i64)%d) + (tg_i64)threadIdx.x * %d, qb = qa + %d;"
+      % (ALIGN - 1, U, B * U))
+    w.open("if (qa < q1)")
+    step("qa", "q0", "q1", "cacc")
+    w.close()
+    w.open("if (qb < q1)")
+    step("qb", "q0", "q1", "cacc2")
+    w.close()
+    w("cacc += cacc2;")
     w("#pragma unroll 1")
-    w.open("for (tg_i64 q = (q0 & ~(tg_i64)%d) + (tg_i64)threadIdx.x * %d; q < q1; q += %d)"
-           % (ALIGN - 1, U, B * U))
+    w.open("for (tg_i64 q = qb + %d; q < q1; q += %d)" % (B * U, B * U))
     step("q", "q0", "q1", "cacc")
     w.close()
     w("cacc = tg_segsum<64>(cacc);")
