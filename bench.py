@@ -22,6 +22,10 @@ cpu_openmp   this build's OpenMP CPU backend (the reference's ``_cpu_emit``
              design) at the reference default schedule T32/TPR1/U1/V1/B128,
              compiled on this host with g++ -O3 -march=native -fopenmp and run
              on every OpenMP thread, host perf_counter around each call
+cpu_openmp_tuned
+             the same backend at the case's CPU-tuned schedule
+             (tilegen_amd.schedules.CPU_TUNED, from tilegen_amd.cpu_tuned);
+             null for a case without one
 
 Cases are BASELINE.json's configs (tilegen_amd.matrices.baseline_ids()); the
 default c1 is the config the headline metric is quoted on.
@@ -143,14 +147,16 @@ def _omp_threads() -> int:
         return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
 
 
-def _openmp_baseline(kernel, A, ops, K, ref, nbytes, nflop, budget_s: float):
-    """Time the OpenMP variant of the reference default schedule on the host."""
+def _openmp_baseline(kernel, A, ops, K, ref, nbytes, nflop, budget_s: float, cfg=None):
+    """Time the OpenMP variant of a schedule on the host (the reference
+    default schedule unless ``cfg`` is given)."""
     from tilegen_amd.autotune import BASELINE, _make_caller, _time_host
     from tilegen_amd.codegen import generate
     from tilegen_amd.dsl import standard_kernels
     from tilegen_amd.verify import compile_generated
+    cfg = cfg or BASELINE
     workdir = os.path.join(ROOT, "build", "bench_cpu")
-    gen = generate(standard_kernels()[kernel], BASELINE, "cpu", outdir=workdir)
+    gen = generate(standard_kernels()[kernel], cfg, "cpu", outdir=workdir)
     so, log = compile_generated(gen, "cpu", workdir)
     data = (ops.get("x"), None, ops.get("B"), ops.get("U"), ops.get("V"), 1.0, 0.0)
     caller, _out, _keep = _make_caller(so, kernel, A, data, K, "cpu")
@@ -162,7 +168,7 @@ def _openmp_baseline(kernel, A, ops, K, ref, nbytes, nflop, budget_s: float):
     ms = _time_host(caller.launch, 2, iters)
     med = float(np.median(ms)) * 1e-3
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": _omp_threads(),
-            "kind": "openmp backend", "schedule": BASELINE.short(),
+            "kind": "openmp backend", "schedule": cfg.short(),
             "sample": "%d calls of the full matrix, median %.3f ms per call" % (iters, med * 1e3),
             "gflops": round(nflop / med / 1e9, 3), "ms_median": round(med * 1e3, 4),
             "ms_min": round(float(np.min(ms)), 4), "rel_err": err,
@@ -317,10 +323,17 @@ def main(argv=None) -> int:
                "gflops": round(nflop / sec / 1e9, 3), "ms_per_call": round(sec * 1e3, 4)}
         _log("cpu baseline (%s): %.3f ms per call" % (kind, sec * 1e3))
 
-    omp = None
+    omp = omp_tuned = None
     if not args.no_cpu:
         omp = _openmp_baseline(case.kernel, A, ops, K, ref, nbytes, nflop, args.cpu_seconds / 2)
         _log("cpu OpenMP backend (%d threads): %s" % (omp["cores"], omp["sample"]))
+        from tilegen_amd.schedules import CPU_TUNED
+        if args.case in CPU_TUNED:
+            omp_tuned = _openmp_baseline(case.kernel, A, ops, K, ref, nbytes, nflop,
+                                         args.cpu_seconds / 2, CPU_TUNED[args.case])
+            omp_tuned["kind"] = "openmp backend, CPU-tuned schedule"
+            _log("cpu OpenMP backend, tuned %s: %s" % (omp_tuned["schedule"],
+                                                      omp_tuned["sample"]))
 
     for bufs in keep:
         for b in bufs.values():
@@ -363,6 +376,7 @@ def main(argv=None) -> int:
         },
         "cpu_baseline": cpu,
         "cpu_openmp": omp,
+        "cpu_openmp_tuned": omp_tuned,
         "vendor": vendor,
         "check_rel_err": err,
         "device": "%s %s" % (dev["name"], dev["arch"]),

@@ -55,3 +55,13 @@ def test_bench_json_line(hip_ready):
     cpu = out["cpu_baseline"]
     assert cpu["kind"] in ("reference", "port") and cpu["cores"] == 1 and cpu["value"] > 0
     assert out["check_rel_err"] <= 1e-10
+
+
+def test_cpu_tuned_schedules_are_row_tiles_of_known_cases():
+    """Every CPU-tuned schedule names a BASELINE case and is a plain row-tile
+    schedule (the OpenMP backend ignores the GPU-only balance)."""
+    from tilegen_amd.matrices import baseline_ids
+    from tilegen_amd.schedules import CPU_TUNED
+    for case_id, cfg in CPU_TUNED.items():
+        assert case_id in baseline_ids()
+        assert cfg.balance == "rows"

@@ -314,8 +314,11 @@ def _time_host(caller, warmup: int, iters: int) -> np.ndarray:
 # search
 # --------------------------------------------------------------------------- #
 def _candidate_configs(kernel: str, K: int, budget: int, mode: str, rng: random.Random,
-                       include: Optional[List[Config]] = None) -> List[Config]:
+                       include: Optional[List[Config]] = None,
+                       backend: str = "hip") -> List[Config]:
     pool = legal_configs(kernel, K)
+    if backend == "cpu":  # the OpenMP emitter ignores balance: row tiles only
+        pool = [c for c in pool if c.balance == "rows"]
     out: List[Config] = []
     seen = set()
 
@@ -335,7 +338,7 @@ def _candidate_configs(kernel: str, K: int, budget: int, mode: str, rng: random.
     if mode == "coordinate":
         best = out[0]
         steps = [(key, value) for key in SEARCH_SPACE for value in SEARCH_SPACE[key]]
-        if kernel in MERGE_KERNELS:
+        if kernel in MERGE_KERNELS and backend != "cpu":
             steps += [("balance", "nnz"), ("balance", "hybrid")]
         for key, value in steps:
             add(Config(**{**best.to_dict(), key: value}))
@@ -372,7 +375,7 @@ def tune(kernel_name: str, matrix, budget: int = 40, mode: str = "random",
     flop, ref_bytes, comp_bytes = _flops_bytes(kernel_name, A, K)
     M, N = A.shape
     nnz = int(A.nnz)
-    candidates = _candidate_configs(kernel_name, K, budget, mode, rng, include)
+    candidates = _candidate_configs(kernel_name, K, budget, mode, rng, include, backend)
     kernels = standard_kernels()
     eps = float(np.finfo(np.float64).eps)
     scale = float(np.abs(ref).max()) if ref.size else 0.0

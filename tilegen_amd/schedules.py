@@ -37,6 +37,20 @@ TUNED: Dict[str, Config] = {
     "c5x25": Config(tile_size=16, threads_per_row=8, unroll=4, vector_width=2, block_size=128),
 }
 
+# CPU-tuned OpenMP schedules per BASELINE case (``python -m tilegen_amd.cpu_tuned``:
+# random search, budget 40, seed 0, on the GPU box's host); bench.py times them
+# beside the reference default T32/TPR1/U1/V1/B128 as the CPU baseline's
+# second OpenMP leg.
+CPU_TUNED: Dict[str, Config] = {
+    "c1": Config(tile_size=8, threads_per_row=32, unroll=2, vector_width=1, block_size=256),
+    "c2": Config(tile_size=16, threads_per_row=16, unroll=2, vector_width=1, block_size=128),
+    "c3a": Config(tile_size=16, threads_per_row=16, unroll=8, vector_width=1, block_size=128),
+    "c3b": Config(tile_size=8, threads_per_row=32, unroll=2, vector_width=1, block_size=256),
+    "c4": Config(tile_size=8, threads_per_row=16, unroll=1, vector_width=1, block_size=128),
+    "c5": Config(tile_size=2, threads_per_row=4, unroll=2, vector_width=2, block_size=64),
+    "c5x25": Config(tile_size=2, threads_per_row=8, unroll=4, vector_width=1, block_size=64),
+}
+
 # Swept by the GPU parity tests for every kernel: every threads_per_row the
 # wave allows, tiles below/at/above the lane-group count, unroll 1..8, both
 # vector widths, and an untiled schedule (reference tests/test_cuda_gpu.py:34-44
