@@ -21,6 +21,7 @@ Around them (the reference's scripts/ and harness, rebuilt for this backend):
     profiling         rocprofv3 summaries for profiles/
     microbench        hardware probes behind the roofline analysis
     skew              row tiles against merge-path windows on skewed matrices
+    cpu_tuned         CPU-tuned OpenMP schedules for the CPU baseline
     build             in-tree native build (libtgrt, harness, oracle, kernel cache)
 """
 

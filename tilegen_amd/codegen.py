@@ -20,7 +20,12 @@ backend "hip"
         only 8-byte aligned take per-element loads); Tile(T) = a
         workgroup owns T rows whose row pointers are staged once in LDS and
         whose first step is issued for every row before any gather, so each
-        wave keeps several rows of loads in flight.
+        wave keeps several rows of loads in flight.  Config.balance picks what
+        a tile holds: T rows ("rows"), an equal merge-path window of rows plus
+        nonzeros ("nnz"), or T rows with the rows longer than B*U nonzeros
+        left to workgroups over equal nonzero ranges ("hybrid"); rows cut
+        across workgroups are combined in a fixed order through module
+        scratch.
     row_dense_out (spmm)
         ThreadsPerRow(k) lanes per output row spread over the K columns,
         Vectorize(2) = 128-bit loads of B rows and stores of C, Unroll(u) =
