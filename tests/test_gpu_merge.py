@@ -101,3 +101,36 @@ def test_merge_path_agrees_with_row_tiles(hip_ready):
             other = Variant("spmv", Config(tile_size=T, threads_per_row=tpr, unroll=U,
                                            block_size=B, balance=balance)).run(A, **ops)
             assert rel_inf(other, rows) <= TOL, (case_id, balance)
+
+
+@pytest.mark.parametrize("cfg", MERGE_TEST_SCHEDULES[:2] + HYBRID_TEST_SCHEDULES[:2],
+                         ids=[schedule_id(c) for c in MERGE_TEST_SCHEDULES[:2] +
+                              HYBRID_TEST_SCHEDULES[:2]])
+@pytest.mark.parametrize("kernel", ["spmv", "fused_spmv_axpy"])
+def test_verify_api_with_balance(kernel, cfg, hip_ready, tmp_path):
+    """The reference's verify() on its 257 x 257 test matrix with merge-path
+    and hybrid schedules: the reference tolerance, the 1e-10 normwise bar and
+    indptr/indices untouched."""
+    from tests.util import mixed_257
+    from tilegen_amd.verify import verify
+    r = verify(kernel, cfg, mixed_257(), backend="hip", workdir=str(tmp_path), K=8)
+    assert r.executed and r.ok, r.message
+    assert r.max_abs_err <= r.tolerance
+    assert r.rel_err_inf <= TOL and r.rel_err_2 <= TOL
+    assert r.structure_intact is True
+
+
+def test_tune_with_balance_candidates(hip_ready, tmp_path):
+    """tune() times and verifies merge-path and hybrid candidates beside row
+    tiles on a skewed matrix; every candidate it ran is correct and the winner
+    is one of them."""
+    from tilegen_amd.autotune import tune
+    A = make_baseline("c3a", scale=0.05)
+    inc = [MERGE_TEST_SCHEDULES[1], HYBRID_TEST_SCHEDULES[1], HYBRID_TEST_SCHEDULES[0]]
+    res = tune("spmv", A, budget=len(inc) + 1, mode="random", backend="hip", include=inc,
+               iters=5, warmup=2, workdir=str(tmp_path))
+    ran = [r for r in res["records"] if r.get("ms_median") is not None]
+    assert len(ran) == len(inc) + 1
+    assert all(r["ok"] for r in ran)
+    assert res["winner"] in [r["config"] for r in ran]
+    assert {r["config"].get("balance", "rows") for r in ran} == {"rows", "nnz", "hybrid"}
