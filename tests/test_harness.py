@@ -81,3 +81,18 @@ def test_hip_backend_device_buffers(kernel, matrix_bin, tmp_path, hip_ready):
     out = json.loads(r.stdout.strip().splitlines()[-1])
     assert out["max_abs_err"] < 1e-12, out
     assert out["timer"] == "dispatch events (tg_time_launches)" and out["ms_min"] > 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("balance", ["nnz", "hybrid"])
+def test_hip_harness_balance_modes(balance, matrix_bin, tmp_path, hip_ready):
+    """The harness takes its grid from tgv_geometry, which counts the hybrid
+    tiles' range workgroups; with windows and ranges of a few rows, the
+    240-nonzero row is cut into pieces, and the result still matches."""
+    so = _lib("spmv", "hip", tmp_path, Config(tile_size=2, threads_per_row=4, unroll=1,
+                                              block_size=64, balance=balance))
+    r = _run("--kernel", "spmv", "--matrix", matrix_bin, "--lib", so, "--backend", "hip",
+             "--iters", 10, "--warmup", 2, "--rotate", 3)
+    assert r.returncode == 0, r.stderr
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert out["max_abs_err"] < 1e-12, out
