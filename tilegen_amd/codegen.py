@@ -816,11 +816,12 @@ __device__ tg_i64 tg_mp_search(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i
 
 // Partial sums of the pieces of rows cut at window edges, two per window w: the
 // piece of the row that begins in w (slot 2w + 1) and of the row that began
-// before it (slot 2w); and per first window, the number of pieces finished.
-// The last piece in zeroes the count, so every launch starts from zero.  Only
-// device-scope atomics touch these; launches that overlap on one device race.
+// before it (slot 2w).  A slot holds 0 when empty and bits(partial) ^ TG_MP_KEY
+// when full; TG_MP_KEY is a signalling-NaN pattern, which no floating-point
+// sum produces, so a full slot is never 0.  Only device-scope atomics touch the
+// slots; launches that overlap on one device race.
+#define TG_MP_KEY 0x7FF4A5A5A5A5A5A5ull
 __device__ unsigned long long tg_mp_part[%(P)d];
-__device__ unsigned int tg_mp_cnt[%(C)d];
 
 // The value must be in a register (so the atomic that produced it has returned)
 // before any later memory operation is issued.
@@ -829,39 +830,49 @@ __device__ __forceinline__ void tg_mp_wait(unsigned long long v) {
 }
 
 // Wave: record window w's piece t of the row whose pieces lie in windows
-// wf..wl.  Lane 0 swaps the partial into its slot and, once that swap has
-// returned, counts the piece in; the piece that completes the count reads every
-// partial back (swapping in zeros), sums them in window order with a fixed
-// reduction tree, zeroes the count and returns true with the sum in *tot.
+// wf..wl.  Lane 0 swaps the partial into its slot; once that swap has
+// returned, the lanes read every slot of the row (compare-and-swaps that never
+// match, so they change nothing).  The piece whose swap is performed last finds every slot
+// full (any other piece's read of its slot came later); it may not be the only
+// one.  A piece that finds them all sums them in window order with a fixed
+// reduction tree, empties them and returns true with the sum in *tot; pieces
+// that find an empty slot return false.  Every combiner computes the same bits,
+// every slot is empty again when the launch ends, and no wave waits for another.
 __device__ bool tg_mp_commit(tg_i64 w, tg_i64 wf, tg_i64 wl, double t, double* tot) {
   const int l = threadIdx.x & 63;
-  unsigned seen = 0;
-  if (l == 0) {
-    tg_mp_wait(__hip_atomic_exchange(tg_mp_part + 2 * w + (w == wf ? 1 : 0),
-                                     (unsigned long long)__double_as_longlong(t),
-                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    seen = __hip_atomic_fetch_add(tg_mp_cnt + wf, 1u, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT);
-  }
-  seen = (unsigned)__shfl((int)seen, 0);
-  if ((tg_i64)seen + 1 != wl - wf + 1) return false;
+  unsigned long long mine = 0;
+  if (l == 0)
+    mine = __hip_atomic_exchange(tg_mp_part + 2 * w + (w == wf ? 1 : 0),
+                                 (unsigned long long)__double_as_longlong(t) ^ TG_MP_KEY,
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  tg_mp_wait(__shfl((long long)mine, 0));
   double sum = 0.0;
   #pragma unroll 1
   for (tg_i64 base = wf; base <= wl; base += 64) {
     const tg_i64 v = base + l;
-    double p = 0.0;
-    if (v <= wl)
-      p = __longlong_as_double((long long)__hip_atomic_exchange(
-          tg_mp_part + 2 * v + (v == wf ? 1 : 0), 0ull, __ATOMIC_RELAXED,
-          __HIP_MEMORY_SCOPE_AGENT));
-    sum += tg_segsum<64>(p);
+    unsigned long long b = TG_MP_KEY;   // lanes past wl count as full, adding 0.0
+    if (v <= wl) {
+      // a compare-and-swap that never matches (no slot holds 1) reads the slot where
+      // the swaps are performed; an idempotent add or or may be turned into a load
+      b = 1ull;
+      __hip_atomic_compare_exchange_strong(tg_mp_part + 2 * v + (v == wf ? 1 : 0), &b, 1ull,
+                                           __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (__ballot(b == 0) != 0) return false;
+    sum += tg_segsum<64>(__longlong_as_double((long long)(b ^ TG_MP_KEY)));
   }
-  if (l == 0)
-    (void)__hip_atomic_exchange(tg_mp_cnt + wf, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  #pragma unroll 1
+  for (tg_i64 base = wf; base <= wl; base += 64) {
+    const tg_i64 v = base + l;
+    if (v <= wl)
+      (void)__hip_atomic_exchange(tg_mp_part + 2 * v + (v == wf ? 1 : 0), 0ull,
+                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   *tot = sum;
   return true;
 }
-""" % {"P": 2 * MERGE_CAP, "C": MERGE_CAP})
+""" % {"P": 2 * MERGE_CAP})
 
 
 def _merge_window(w: _W, TR: int, WAVES: int) -> None:
