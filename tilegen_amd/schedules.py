@@ -23,11 +23,13 @@ TUNED: Dict[str, Config] = {
     # skewed rows.  c3a: hybrid tiles, rows over 1024 nonzeros (half of a
     # 2 x 256 x 4 range) summed by long-row workgroups over equal nonzero ranges,
     # the rest on 4-lane groups (13.7 us against 17.4 with row tiles alone).
-    # c3b: row tiles, short rows on 32-lane groups, rows over 8 group steps (512
-    # nonzeros) taken by the whole workgroup (hybrid tiles tie at 10.4 us)
+    # c3b: hybrid tiles, rows over 512 nonzeros on ranges of 1024, the rest in
+    # tiles of 128 rows on 2-lane groups (10.3 us against 10.6 for the best row
+    # tiles, T32/TPR32/U2/B1024, in three interleaved repeats on one box)
     "c3a": Config(tile_size=64, threads_per_row=4, unroll=4, vector_width=1, block_size=256,
                   balance="hybrid"),
-    "c3b": Config(tile_size=32, threads_per_row=32, unroll=2, vector_width=1, block_size=1024),
+    "c3b": Config(tile_size=128, threads_per_row=2, unroll=2, vector_width=1, block_size=256,
+                  balance="hybrid"),
     # K = 64: 16 lanes x 2 columns x 2 passes per row, 2 nonzeros' B rows in flight
     "c4": Config(tile_size=16, threads_per_row=16, unroll=2, vector_width=2, block_size=64),
     # K = 64 on the chunked SDDMM path: 8 lanes per row x 2 columns per load x 4
