@@ -13,7 +13,7 @@ last rows, mostly empty rows, power-law and dense-row patterns, and more
 windows than the scratch holds (rows past it are summed whole).  Every result
 must meet the 1e-10 normwise bar against the C oracle and float64 SciPy, and
 launching again onto NaN-filled outputs must give the same bits (the piece
-order is fixed and every count is back at zero).  Launches go through
+order is fixed and every partial slot is empty again).  Launches go through
 ``launch_<name>`` with device pointers.
 """
 
@@ -66,6 +66,20 @@ def test_merge_path_matches_oracle(kernel, cfg, hip_ready):
                                                       A.shape[0], A.nnz), flush=True)
         out = _check(kernel, cfg, A, K=1, label=label)
         _again_onto_nan(kernel, cfg, A, out)
+
+
+@pytest.mark.parametrize("balance", ["nnz", "hybrid"])
+def test_zero_rows_launch_nothing(balance, hip_ready):
+    """No rows and no nonzeros make an empty grid: the launcher returns before
+    any kernel runs, and the next launch of the same variant is unaffected."""
+    v = Variant("spmv", Config(tile_size=64, threads_per_row=4, unroll=4, block_size=256,
+                               balance=balance))
+    out = v.run(csr(0, 4, np.zeros(1, dtype=np.int64), [], []), x=np.ones(4))
+    assert out.shape == (0,)
+    A = _cases()["huge_first_and_last"]
+    x = _operands("spmv", A, 1)["x"]
+    got = v.run(A, x=x)
+    assert rel_inf(got, A @ x) <= TOL
 
 
 def test_merge_path_more_windows_than_scratch(hip_ready):
