@@ -8,6 +8,7 @@ import json
 import os
 
 import numpy as np
+import pytest
 
 from tests.util import ragged
 from tilegen_amd import tune_all, verify_all
@@ -26,10 +27,25 @@ def test_verify_all_cpu(tmp_path):
                              workdir=str(tmp_path / "gen"), log=lambda m: None)
     s = payload["summary"]
     assert s["normal_triples"] == len(verify_all.KERNELS) * len(verify_all.CONFIGS)
+    assert s["balance_triples"] == 0   # the OpenMP emitter has row tiles only
     assert s["all_normal_passed"] and s["all_bugs_caught"] and s["bug_triples"] == 1
     assert s["max_rel_err_inf"] <= 1e-10
     md = verify_all.render_table(payload)
     assert md.count("| tiny |") == s["total_triples"] and "| yes |" in md
+
+
+@pytest.mark.gpu
+def test_verify_all_hip_balance_forms(tmp_path, hip_ready):
+    """On the HIP backend spmv also runs in its merge-path and hybrid forms."""
+    _write_tiny(str(tmp_path))
+    payload = verify_all.run(str(tmp_path), "hip", classes=["tiny"], kernels=["spmv"],
+                             workdir=str(tmp_path / "gen"), log=lambda m: None)
+    s = payload["summary"]
+    assert s["executed"] and s["balance_triples"] == len(verify_all.BALANCE_CONFIGS)
+    assert s["normal_triples"] == len(verify_all.CONFIGS) + len(verify_all.BALANCE_CONFIGS)
+    assert s["all_normal_passed"] and s["all_bugs_caught"]
+    md = verify_all.render_table(payload)
+    assert md.count("/hybrid |") == 2 and md.count("/nnz |") == 2
 
 
 def test_tune_all_cpu(tmp_path):

@@ -445,7 +445,7 @@ def ms_median_or(v: float) -> float:
 _METRIC_FIELDS = ["ms_mean", "ms_min", "ms_median", "gflops", "bandwidth_gbs",
                   "compulsory_gbs", "max_abs_err", "tolerance", "ok", "speedup_vs_naive"]
 _CSV_COLS = ["matrix_class", "kernel", "tile_size", "threads_per_row", "unroll",
-             "vector_width", "block_size", "ms_mean", "ms_min", "ms_median", "gflops",
+             "vector_width", "block_size", "balance", "ms_mean", "ms_min", "ms_median", "gflops",
              "bandwidth_gbs", "compulsory_gbs", "max_abs_err", "ok", "speedup_vs_naive"]
 
 
@@ -456,7 +456,8 @@ def _compact(record: Optional[Dict[str, Any]]) -> Optional[Dict[str, Any]]:
 
 
 def _flat(record: Dict[str, Any]) -> Dict[str, Any]:
-    row = {"matrix_class": record["matrix_class"], "kernel": record["kernel"]}
+    row = {"matrix_class": record["matrix_class"], "kernel": record["kernel"],
+           "balance": "rows"}   # Config.to_dict leaves the default balance out
     row.update(record["config"])
     row.update({k: record.get(k) for k in _METRIC_FIELDS if k in record})
     return row
