@@ -1,4 +1,4 @@
-"""Row tiles against merge-path windows (``python -m tilegen_amd.skew``)."""
+"""Row tiles, merge-path windows and hybrid tiles (``python -m tilegen_amd.skew``)."""
 
 from __future__ import annotations
 
@@ -21,12 +21,13 @@ def test_skew_matrices_have_the_stated_shapes():
     assert (np.diff(m["ten full rows, 8 elsewhere"].indptr) == n).sum() == 10
 
 
-def test_render_pairs_the_two_forms():
+def test_render_lines_up_the_three_forms():
     rows = [{"matrix": "m", "rows": 10, "nnz": 99, "max_row": 10, "schedule": "T16/TPR8/U2/V1/B128",
              "balance": b, "us": us, "rel_err": 0.0, "copies": 2}
-            for b, us in (("rows", 40.0), ("nnz", 10.0))]
+            for b, us in (("rows", 40.0), ("nnz", 10.0), ("hybrid", 20.0))]
     md = skew.render(rows, "x")
-    assert "| m | 10 | 99 | 10 | T16/TPR8/U2/V1/B128 | 40.00 | 10.00 | 0.25 |" in md
+    assert ("| m | 10 | 99 | 10 | T16/TPR8/U2/V1/B128 | 40.00 | 10.00 | 20.00 | 0.25 | 0.50 |"
+            in md)
 
 
 @pytest.mark.gpu
@@ -34,4 +35,4 @@ def test_skew_compare_runs(hip_ready):
     # compare() checks each result against float64 SciPy before it reports a time
     mats = dict(list(skew.skew_matrices(scale=0.02).items())[:2])
     rows = skew.compare(mats, schedules=skew.SCHEDULES[:1], iters=3, rotate_mb=8)
-    assert len(rows) == 4 and all(r["us"] > 0 and r["rel_err"] <= 1e-10 for r in rows)
+    assert len(rows) == 2 * len(skew.FORMS) and all(r["us"] > 0 and r["rel_err"] <= 1e-10 for r in rows)

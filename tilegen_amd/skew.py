@@ -1,9 +1,11 @@
-"""Row tiles against merge-path windows on skewed matrices.
+"""Row tiles, merge-path windows and hybrid tiles on skewed matrices.
 
-Every tiled SpMV schedule comes in two forms (``Config.balance``): tiles of T
-consecutive rows, and merge-path windows that give each workgroup an equal
-share of rows plus nonzeros and cut rows longer than a window into pieces.
-This driver times both forms of the same schedules on matrices whose rows
+Every tiled SpMV schedule comes in three forms (``Config.balance``): tiles of
+T consecutive rows; merge-path windows that give each workgroup an equal
+share of rows plus nonzeros and cut rows longer than a window into pieces; and
+hybrid tiles, row tiles that leave rows longer than B*U nonzeros to extra
+workgroups over equal nonzero ranges.
+This driver times the three forms of the same schedules on matrices whose rows
 range from a few nonzeros to the full width, next to the BASELINE skewed
 cases, and checks every result against float64 SciPy (normwise relative
 error <= 1e-10) before reporting a time.
@@ -33,10 +35,12 @@ from .variant import Variant
 __all__ = ["skew_matrices", "SCHEDULES", "compare", "render", "main"]
 
 TOL = 1e-10
+FORMS = ("rows", "nnz", "hybrid")
 SCHEDULES = [
     Config(tile_size=64, threads_per_row=8, unroll=2, block_size=512),
     Config(tile_size=16, threads_per_row=8, unroll=2, block_size=128),
     Config(tile_size=64, threads_per_row=1, unroll=2, block_size=256),
+    Config(tile_size=64, threads_per_row=4, unroll=4, block_size=256),   # tuned for c3a
 ]
 
 
@@ -89,7 +93,7 @@ def compare(matrices: Dict[str, sp.csr_matrix], schedules=SCHEDULES, iters: int 
                 for _ in range(copies)]
         try:
             for cfg in schedules:
-                for balance in ("rows", "nnz"):
+                for balance in FORMS:
                     c = Config(**{**cfg.to_dict(), "balance": balance})
                     v = Variant("spmv", c)
                     g, b, lds = v.geometry(M, N, 0, A.nnz)
@@ -115,23 +119,26 @@ def compare(matrices: Dict[str, sp.csr_matrix], schedules=SCHEDULES, iters: int 
 
 
 def render(rows: List[dict], device: str) -> str:
-    md = ["# Row tiles against merge-path windows (%s)" % device, "",
+    md = ["# Row tiles, merge-path windows and hybrid tiles (%s)" % device, "",
           "Written by `python -m tilegen_amd.skew`; SpMV kernel medians of dispatch-attached "
           "events over cold (rotated) inputs, each result within 1e-10 of float64 SciPy.", "",
           "| matrix | rows | nnz | longest row | schedule | row tiles µs | merge windows µs | "
-          "merge / rows |", "|---|---:|---:|---:|---|---:|---:|---:|"]
+          "hybrid tiles µs | merge / rows | hybrid / rows |",
+          "|---|---:|---:|---:|---|---:|---:|---:|---:|---:|"]
     by = {}
     for r in rows:
         by.setdefault((r["matrix"], r["schedule"]), {})[r["balance"]] = r
     for (m, s), d in by.items():
-        a, b = d["rows"], d["nnz"]
-        md.append("| %s | %d | %d | %d | %s | %.2f | %.2f | %.2f |" % (
-            m, a["rows"], a["nnz"], a["max_row"], s, a["us"], b["us"], b["us"] / a["us"]))
+        a = d["rows"]
+        cells = ["%.2f" % d[f]["us"] if f in d else "-" for f in FORMS]
+        ratios = ["%.2f" % (d[f]["us"] / a["us"]) if f in d else "-" for f in FORMS[1:]]
+        md.append("| %s | %d | %d | %d | %s | %s |" % (
+            m, a["rows"], a["nnz"], a["max_row"], s, " | ".join(cells + ratios)))
     return "\n".join(md) + "\n"
 
 
 def main(argv=None) -> int:
-    ap = argparse.ArgumentParser(description="Row tiles vs merge-path windows on skew.")
+    ap = argparse.ArgumentParser(description="Row tiles, merge windows, hybrid tiles on skew.")
     ap.add_argument("--out", default="results")
     ap.add_argument("--scale", type=float, default=1.0)
     a = ap.parse_args(argv)
