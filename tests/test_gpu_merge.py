@@ -10,7 +10,7 @@ same piece combine.  The matrices put that logic at its edges: no
 nonzeros, one row, rows ending exactly at the last nonzero, a row spanning
 hundreds of windows (more than one wave of pieces to combine), long first and
 last rows, mostly empty rows, power-law and dense-row patterns, and more
-windows than the scratch holds (rows past it are summed whole).  Every result
+windows or ranges than the scratch holds (rows past it are summed whole).  Every result
 must meet the 1e-10 normwise bar against the C oracle and float64 SciPy, and
 launching again onto NaN-filled outputs must give the same bits (the piece
 order is fixed and every partial slot is empty again).  Launches go through
@@ -98,6 +98,25 @@ def test_merge_path_more_windows_than_scratch(hip_ready):
     print("[gpu] merge scratch capacity rows=%d nnz=%d windows=%d" % (rows, A.nnz, G),
           flush=True)
     out = _check("spmv", cfg, A, K=1, label="past_scratch")
+    _again_onto_nan("spmv", cfg, A, out)
+
+
+def test_hybrid_more_ranges_than_scratch(hip_ready):
+    """70357 ranges of 128 nonzeros against 65536 scratch slots: the long row
+    near the top is cut into pieces combined through the scratch; the one near
+    the bottom, and every row over 64 nonzeros that reaches past the last slot,
+    is summed whole by the range it begins in."""
+    rows = 150_000
+    A = ragged(37, rows, 512, 120, long_rows=[(10, 512), (rows - 50, 512)])
+    cfg = Config(tile_size=64, threads_per_row=4, unroll=1, block_size=64, balance="hybrid")
+    CH = Variant("spmv", cfg).gen.geometry.nnz_chunk
+    assert CH == 128 and -(-A.nnz // CH) > cg.MERGE_CAP
+    ip = A.indptr
+    assert 0 < (ip[11] - 1) // CH - ip[10] // CH and (ip[11] - 1) // CH < cg.MERGE_CAP
+    assert ip[rows - 50] // CH < (ip[rows - 49] - 1) // CH and ip[rows - 50] // CH >= cg.MERGE_CAP
+    print("[gpu] hybrid scratch capacity rows=%d nnz=%d ranges=%d" % (rows, A.nnz, -(-A.nnz // CH)),
+          flush=True)
+    out = _check("spmv", cfg, A, K=1, label="hybrid_past_scratch")
     _again_onto_nan("spmv", cfg, A, out)
 
 
