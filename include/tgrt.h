@@ -77,6 +77,18 @@ int tg_function_attrs(tg_function fn, int* num_regs, int* lds_bytes, int* scratc
 int tg_launch(tg_function fn, int64_t grid, int32_t block, int32_t lds_bytes,
               const uint64_t* args, int n_args, void* stream, int sync);
 
+/* tg_launch, ordered after the previous launch made with the same order_key on
+ * the current device: when that launch went to another stream, `stream` first
+ * waits for its end (an event recorded after every such launch).  Generated
+ * launchers of kernels that combine row pieces through module scratch pass
+ * their embedded code object as the key, so calls that overlap on two streams
+ * run one after the other instead of racing on the scratch.  A launch into a
+ * stream under graph capture is passed to tg_launch unordered.  No counterpart
+ * in the reference, whose launchers are synchronous on the null stream. */
+int tg_launch_ordered(const void* order_key, tg_function fn, int64_t grid, int32_t block,
+                      int32_t lds_bytes, const uint64_t* args, int n_args, void* stream,
+                      int sync);
+
 /* GPU-side timing. Launches `warmup` + `iters` times on `stream`, launch i
  * using argument set (i % n_sets) of `arg_sets` (n_sets x n_args slots), so a
  * caller can rotate among input copies that do not fit in cache together.

@@ -16,7 +16,8 @@ import oracle
 from tests.util import csr, mixed_257, ragged, rel_2, rel_inf
 from tilegen_amd.codegen import Config
 from tilegen_amd.matrices import make_baseline
-from tilegen_amd.schedules import TEST_KERNELS, TEST_SCHEDULES, schedule_id
+from tilegen_amd.schedules import (ODD_BLOCK_SCHEDULES, TEST_KERNELS, TEST_SCHEDULES,
+                                   schedule_id)
 from tilegen_amd import runtime as rt
 from tilegen_amd.variant import Variant, operand_order
 from tilegen_amd.verify import _inputs_for, _reference, verify
@@ -94,6 +95,19 @@ def test_injected_bug_is_caught(kernel, hip_ready, tmp_path):
     assert r.executed and "compile error" not in r.message, r.message
     assert not r.ok, "%s: injected bug not detected" % kernel
     assert r.max_abs_err > r.tolerance
+
+
+@pytest.mark.parametrize("kernel", TEST_KERNELS)
+@pytest.mark.parametrize("cfg", ODD_BLOCK_SCHEDULES,
+                         ids=[schedule_id(c) for c in ODD_BLOCK_SCHEDULES])
+def test_block_sizes_not_a_power_of_two(kernel, cfg, hip_ready):
+    """3, 5 and 7 waves per workgroup; rows long enough to leave their lane
+    group, so SpMM's long-row tree combines 3, 28, 40 and 96 slices."""
+    long_rows = ragged(8, 2500, 2500, 6, empty_every=7,
+                       long_rows=[(5, 2000), (150, 700), (2499, 129)])
+    for label, A in (("mixed_257", mixed_257()), ("long_rows", long_rows)):
+        print("[gpu] odd-block %s %s %s" % (kernel, cfg.short(), label), flush=True)
+        _check(kernel, cfg, A, K=64, label=label)
 
 
 SPMV_CFGS = [

@@ -5,6 +5,9 @@ No GPU: HIP sources are checked as text and compiled by hipRTC for gfx950."""
 from __future__ import annotations
 
 import os
+import re
+
+import numpy as np
 
 import pytest
 
@@ -320,3 +323,96 @@ def test_spmm_sddmm_long_rows_relative_to_the_tile():
     assert "((len) > 64 && ((len) * t_rows > 2 * t_nnz || (len) > 128))" in sddmm
     assert "s_tnnz = t_end > row0 ? indptr[t_end] - indptr[row0] : 0;" in sddmm
 
+
+
+# --------------------------------------------------------------------------- #
+# SpMM long-row combine: the emitted fixed-order tree over the lane groups'
+# partial C-row slices, executed here on integers
+# --------------------------------------------------------------------------- #
+_TREE = re.compile(r"for \(int e = threadIdx\.x; e < (\d+); e \+= (\d+)\) "
+                   r"s_part\[e\] \+= s_part\[e \+ (\d+)\];")
+
+
+def _tree_groups(src):
+    """Each combine (one per vector width) as its list of (limit, offset)."""
+    groups, cur = [], None
+    for line in src.splitlines():
+        if "fixed-order tree over the lane groups' partial slices" in line:
+            cur = []
+            groups.append(cur)
+            continue
+        m = _TREE.search(line)
+        if m and cur is not None:
+            cur.append((int(m.group(1)), int(m.group(3))))
+    return groups
+
+
+def _run_tree(steps, slots, cols, seed=0):
+    """Execute the tree with the lanes' parallel semantics (every read sees
+    the level's input); returns the first ``cols`` entries and the exact sums."""
+    rng = np.random.default_rng(seed)
+    part = [int(v) for v in rng.integers(-2**40, 2**40, size=slots * cols)]
+    want = [sum(part[s * cols + c] for s in range(slots)) for c in range(cols)]
+    for limit, off in steps:
+        assert limit + off <= slots * cols
+        assert limit <= off, "a level reads what it writes"
+        part = [part[e] + part[e + off] if e < limit else part[e] for e in range(len(part))]
+    return part[:cols], want
+
+
+@pytest.mark.parametrize("block,tpr", [(64, 64), (192, 64), (320, 8), (448, 16), (576, 32),
+                                       (960, 64), (1024, 8), (384, 4), (704, 1)])
+def test_spmm_long_row_tree_sums_every_slice(block, tpr):
+    """Block sizes whose lane-group count is not a power of two (3, 5, 7 ...
+    waves) keep every slice: the tree folds the upper ceil(n/2) slices onto the
+    lower floor(n/2) at each level."""
+    cfg = Config(tile_size=2 * (block // tpr), threads_per_row=tpr, unroll=1, vector_width=2,
+                 block_size=block)
+    groups = _tree_groups(_hip("spmm", cfg))
+    assert len(groups) == 2  # 128-bit and scalar paths
+    slots = block // tpr
+    for steps, cols in zip(groups, (2 * tpr, tpr)):
+        got, want = _run_tree(steps, slots, cols)
+        assert got == want, (block, tpr, cols)
+
+
+def test_tree_simulation_catches_a_dropped_slice():
+    """The power-of-two halving (n //= 2) loses the middle slice of 3."""
+    cols, slots = 4, 3
+    halving = [(1 * cols, 1 * cols)]  # 3 // 2 = 1 level
+    got, want = _run_tree(halving, slots, cols)
+    assert got != want
+
+
+@pytest.mark.parametrize("dtype", ["f32", "float", "f16"])
+def test_hip_refuses_non_f64_accumulator(dtype):
+    cfg = Config(tile_size=32, threads_per_row=4, unroll=2, block_size=256, dtype=dtype)
+    with pytest.raises(ValueError, match="float64 only"):
+        _hip("spmv", cfg)
+    with pytest.raises(ValueError, match="float64 only"):
+        generate(standard_kernels()["spmm"], cfg, "hip", write=False)
+    # the CPU backend declares its accumulator in that type, as the reference does
+    if dtype != "f16":
+        src = generate(standard_kernels()["spmv"], cfg, "cpu", write=False).source
+        assert "float acc" in src
+
+
+def test_hip_verify_reports_non_f64_as_compile_error(tmp_path):
+    from tilegen_amd.verify import verify
+    from tests.util import mixed_257
+    r = verify("spmv", Config(dtype="f32"), mixed_257(), backend="hip", workdir=str(tmp_path))
+    assert not r.ok and "float64 only" in r.message
+
+
+@pytest.mark.parametrize("balance,ordered", [("rows", False), ("nnz", True), ("hybrid", True)])
+def test_scratch_modules_launch_in_order(balance, ordered):
+    """Merge-path and hybrid modules share one scratch per device: their
+    launchers order each launch after the previous one on any stream."""
+    cfg = Config(tile_size=64, threads_per_row=4, unroll=4, block_size=256, balance=balance)
+    for name in ("spmv", "fused_spmv_axpy"):
+        k = _run(standard_kernels()[name], cfg, "hip")
+        host = emit_hip_host(k, cfg)
+        async_fn = host.split("int tgv_launch_async(")[1].split("\n}\n")[0]
+        assert ("tg_launch_ordered(tg_code, fn," in async_fn) == ordered
+        assert ("return tg_launch(fn," in async_fn) == (not ordered)
+        assert ("tg_mp_part" in emit_hip(k, cfg)) == ordered

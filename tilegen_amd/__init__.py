@@ -19,8 +19,6 @@ Around them (the reference's scripts/ and harness, rebuilt for this backend):
     ablation          per-pass contribution (code diff, verify, GPU timing)
     vendor            rocSPARSE SpMV timing beside the tuned kernel
     profiling         rocprofv3 summaries for profiles/
-    microbench        hardware probes behind the roofline analysis
-    skew              row tiles, merge-path windows and hybrid tiles on skew
     cpu_tuned         CPU-tuned OpenMP schedules for the CPU baseline
     build             in-tree native build (libtgrt, harness, oracle, kernel cache)
 """

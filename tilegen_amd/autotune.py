@@ -10,7 +10,9 @@ one (reference ``autotune.py:47-72``):
   and T > 8*B/TPR makes a lane group walk more than 8 rows in sequence;
 * unroll U in {1, 2, 4, 8}; vector_width V in {1, 2} (2 x f64 = 128 bits,
   the widest global load);
-* LDS per workgroup (8*(T+1) bytes of staged row pointers) within 64 KiB.
+* LDS per workgroup within gfx950's 160 KiB: a tiled SpMV-shaped variant
+  declares about 16 bytes per tile row (staged row pointers plus the long- and
+  medium-row lists), so T <= 2048 stays far inside it.
 
 ``tune(..., backend="hip")`` times each variant with GPU events attached to
 the kernel dispatch (libtgrt ``tg_time_launches``), rotating over enough
@@ -60,7 +62,7 @@ SEARCH_SPACE: Dict[str, List[int]] = {
 BASELINE = Config(tile_size=32, threads_per_row=1, unroll=1, vector_width=1, block_size=128)
 
 _WAVE = 64
-_LDS_LIMIT = 64 * 1024
+_LDS_LIMIT = 160 * 1024  # LDS per CU on gfx950, all of which one workgroup may take
 # kernels whose schedules also come with merge-path windows and hybrid tiles
 # (Config.balance)
 MERGE_KERNELS = ("spmv", "fused_spmv_axpy")
@@ -96,8 +98,8 @@ def illegal_reason(cfg: Config) -> Optional[str]:
         return "tile_size (%d) < lane groups per block (%d): idle lanes" % (T, slots)
     if T > 8 * slots:
         return "tile_size (%d) > 8 rows per lane group (%d groups)" % (T, slots)
-    if 8 * (T + 1) > _LDS_LIMIT:
-        return "staged row pointers (%d B) exceed 64 KiB of LDS" % (8 * (T + 1))
+    if 16 * (T + 1) > _LDS_LIMIT:
+        return "row pointers and row lists (%d B) exceed 160 KiB of LDS" % (16 * (T + 1))
     return None
 
 

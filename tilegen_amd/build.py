@@ -89,8 +89,8 @@ def warm_cache(verbose: bool = False) -> int:
     from .dsl import standard_kernels
     from .matrices import baseline_case
     from .passes import PASS_NAMES
-    from .schedules import (HYBRID_TEST_SCHEDULES, MERGE_TEST_SCHEDULES, TEST_KERNELS,
-                            TEST_SCHEDULES, TUNED)
+    from .schedules import (HYBRID_TEST_SCHEDULES, MERGE_TEST_SCHEDULES, ODD_BLOCK_SCHEDULES,
+                            TEST_KERNELS, TEST_SCHEDULES, TUNED)
     from .verify import compile_generated
 
     kernels = standard_kernels()
@@ -98,7 +98,7 @@ def warm_cache(verbose: bool = False) -> int:
     for case_id, cfg in TUNED.items():
         todo.append((baseline_case(case_id).kernel, cfg, ()))
     for name in TEST_KERNELS:
-        for cfg in TEST_SCHEDULES:
+        for cfg in TEST_SCHEDULES + ODD_BLOCK_SCHEDULES:
             todo.append((name, cfg, ()))
         todo.append((name, Config(tile_size=32, threads_per_row=4, unroll=2, vector_width=1,
                                   block_size=256, inject_bug=True), ()))

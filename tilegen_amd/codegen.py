@@ -716,6 +716,13 @@ def launch_geometry(plan: Plan, low: Lowering) -> LaunchGeometry:
     return LaunchGeometry(rows, B, lds, plan.row_extent, chunk)
 
 
+def module_scratch(plan: Plan, low: Lowering) -> bool:
+    """Whether the variant's module keeps row-piece partials in its scratch
+    (merge-path windows and hybrid tiles), so that launches of it must not
+    overlap on one device."""
+    return plan.kind == "scalar_reduce" and low.tiled and low.balance in ("nnz", "hybrid")
+
+
 def hybrid_chunk(low: Lowering) -> int:
     """Nonzeros per long-row workgroup of hybrid tiles: two passes of the whole
     workgroup; rows longer than half of it are summed by those workgroups."""
@@ -819,7 +826,8 @@ __device__ tg_i64 tg_mp_search(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i
 // before it (slot 2w).  A slot holds 0 when empty and bits(partial) ^ TG_MP_KEY
 // when full; TG_MP_KEY is a signalling-NaN pattern, which no floating-point
 // sum produces, so a full slot is never 0.  Only device-scope atomics touch the
-// slots; launches that overlap on one device race.
+// slots.  Two launches of this module must not overlap on one device: the host
+// launcher orders each launch after the previous one (tg_launch_ordered).
 #define TG_MP_KEY 0x7FF4A5A5A5A5A5A5ull
 __device__ unsigned long long tg_mp_part[%(P)d];
 
@@ -1483,12 +1491,15 @@ def _hip_row_dense_out(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
             w("s_part[slot * %d + lane * 2 + 1] = a1;" % cols)
         w("__syncthreads();")
         w("// fixed-order tree over the lane groups' partial slices")
-        s_ = SLOTS // 2
-        while s_ >= 1:
+        # n slices left: the upper ceil(n/2) fold onto the lower floor(n/2), so an odd
+        # count (a block of 3, 5, 6, 7 ... waves) keeps its middle slice for the next level
+        n_ = SLOTS
+        while n_ > 1:
+            h_ = (n_ + 1) // 2
             w("for (int e = threadIdx.x; e < %d; e += %d) s_part[e] += s_part[e + %d];"
-              % (s_ * cols, B, s_ * cols))
+              % ((n_ - h_) * cols, B, h_ * cols))
             w("__syncthreads();")
-            s_ //= 2
+            n_ = h_
         w.open("for (int t = threadIdx.x; t < %d; t += %d)" % (cols, B))
         w("if (kc + t < %s) __builtin_nontemporal_store(s_part[t], %s + row * %s + kc + t);"
           % (kext, out_name, kext))
@@ -1822,8 +1833,19 @@ def _hip_kernel_text(kernel: Kernel, config: Config, plan: Plan, low: Lowering,
     return pre.text() + ("\n" if pre.lines else "") + w.text()
 
 
+def _check_hip_dtype(config: Config) -> None:
+    """The HIP kernels accumulate in float64 only.  The reference declares its
+    accumulator in ``Config.dtype`` (reference ``codegen.py:416``, ``:565``); a
+    request for another type is refused rather than silently given float64."""
+    if config.dtype not in ("f64", "double"):
+        raise ValueError("the HIP backend accumulates in float64 only; Config.dtype=%r is "
+                         "not supported (use the cpu backend for a %s accumulator)"
+                         % (config.dtype, config.dtype))
+
+
 def emit_hip(kernel: Kernel, config: Config) -> str:
     """Device translation unit of a lowered kernel (hipRTC input)."""
+    _check_hip_dtype(config)
     plan, low = _plan(kernel), _lowering(kernel)
     if config.balance != "rows" and config.tile_size <= 1:
         raise ValueError("balance '%s' needs a tile (tile_size > 1); %s is untiled"
@@ -1847,8 +1869,12 @@ def emit_hip_host(kernel: Kernel, config: Config) -> str:
     when the variant is built.  The launcher exports the reference ABI
     (synchronous, device pointers, errors reported through ``tg_last_error``)
     plus ``tgv_geometry``, ``tgv_function`` and ``tgv_launch_async`` for
-    harnesses that time the kernel on their own stream.
+    harnesses that time the kernel on their own stream.  Variants that combine
+    row pieces through module scratch (``module_scratch``) launch through
+    ``tg_launch_ordered`` keyed by their code object, so calls on different
+    streams never overlap on the scratch.
     """
+    _check_hip_dtype(config)
     plan, low = _plan(kernel), _lowering(kernel)
     sig, args, _info = abi_of(kernel)
     geo = launch_geometry(plan, low)
@@ -1864,6 +1890,7 @@ def emit_hip_host(kernel: Kernel, config: Config) -> str:
             pack.append("  memcpy(&a[%d], &%s, sizeof(double));" % (len(pack), n))
         else:
             pack.append("  a[%d] = (uint64_t)%s;" % (len(pack), n))
+    uses_scratch = module_scratch(plan, low)
     kdim = "K" if "K" in dims else "0"
     ndim = "N" if "N" in dims else "0"
     nnz = "nnz" if "nnz" in dims else "0"
@@ -1912,8 +1939,7 @@ int tgv_launch_async(void* stream, %(params)s) {
   tgv_geometry(%(M)s, %(N)s, %(K)s, %(nnz)s, &grid, &block, &lds);
   if (grid == 0) return 0;
   uint64_t a[%(nargs)d];
-  int n = tgv_pack(a, %(names)s);
-  return tg_launch(fn, grid, block, lds, a, n, stream, 0);
+  int n = tgv_pack(a, %(names)s);%(launch)s
 }
 
 %(sig)s {
@@ -1927,6 +1953,11 @@ int tgv_launch_async(void* stream, %(params)s) {
         "pack": "\n".join(pack), "nargs": len(args), "names": ", ".join(names),
         "sig": sig, "M": "M" if "M" in dims else "0", "N": ndim, "K": kdim, "nnz": nnz,
         "extra_grid": " + ceil(nnz / %d)" % geo.nnz_chunk if geo.nnz_chunk else "",
+        "launch": ("\n  /* row pieces are combined through this module's scratch, which one launch"
+                   "\n     at a time may use: order after its previous launch on any stream */"
+                   "\n  return tg_launch_ordered(tg_code, fn, grid, block, lds, a, n, stream, 0);"
+                   if uses_scratch else
+                   "\n  return tg_launch(fn, grid, block, lds, a, n, stream, 0);"),
         "extra": ("\n  /* long-row workgroups of hybrid tiles, ahead of the row tiles */"
                   "\n  if (*grid > 0 && nnz > 0) *grid += (nnz + %d - 1) / %d;"
                   % (geo.nnz_chunk, geo.nnz_chunk)) if geo.nnz_chunk else "",

@@ -81,6 +81,23 @@ CodeCache& code_cache() {
   return *c;
 }
 
+// Launch order of tg_launch_ordered: key = (caller's order key, device).  The
+// event marks the end of the key's latest launch, which went to `last`.
+struct OrderState {
+  hipEvent_t done = nullptr;
+  hipStream_t last = nullptr;
+  bool pending = false;
+};
+struct OrderTable {
+  std::mutex mu;
+  std::map<std::pair<const void*, int>, OrderState> keys;
+};
+// Never destroyed, like the code cache (tg_code_release drops entries at exit).
+OrderTable& order_table() {
+  static OrderTable* t = new OrderTable;
+  return *t;
+}
+
 bool valid_geometry(int64_t grid, int32_t block) {
   if (grid <= 0 || block <= 0 || block > 1024) return false;
   // the dispatch packet's grid size is a 32-bit count of work-items
@@ -255,6 +272,14 @@ int tg_code_function(const void* code, size_t code_size, const char* name,
 }
 
 int tg_code_release(const void* code, size_t code_size) {
+  {
+    // launch order kept under this code object's address (its event is left
+    // alive: this may run during process exit, so no HIP call is made)
+    OrderTable& t = order_table();
+    std::lock_guard<std::mutex> lock(t.mu);
+    for (auto it = t.keys.begin(); it != t.keys.end();)
+      it = it->first.first == code ? t.keys.erase(it) : std::next(it);
+  }
   CodeCache& c = code_cache();
   std::lock_guard<std::mutex> lock(c.mu);
   for (auto it = c.modules.begin(); it != c.modules.end();) {
@@ -299,6 +324,41 @@ int tg_launch(tg_function fn, int64_t grid, int32_t block, int32_t lds_bytes,
                                static_cast<unsigned>(block), 1, 1,
                                static_cast<unsigned>(lds_bytes), s, params, nullptr),
          "hipModuleLaunchKernel");
+  if (sync) TG_HIP(s ? hipStreamSynchronize(s) : hipDeviceSynchronize(), "synchronize");
+  return 0;
+}
+
+int tg_launch_ordered(const void* order_key, tg_function fn, int64_t grid, int32_t block,
+                      int32_t lds_bytes, const uint64_t* args, int n_args, void* stream,
+                      int sync) {
+  if (!order_key) return fail(-1, "tg_launch_ordered: null order key");
+  if (!fn) return fail(-1, "tg_launch_ordered: null function");
+  if (grid == 0) return 0;
+  int device = 0;
+  TG_HIP(hipGetDevice(&device), "hipGetDevice");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  // the null stream is never captured
+  if (s) TG_HIP(hipStreamIsCapturing(s, &cap), "hipStreamIsCapturing");
+  if (cap != hipStreamCaptureStatusNone) {
+    // a captured launch runs when its graph is replayed, so ordering it
+    // against eager launches here would be meaningless; the graph orders its
+    // own nodes
+    return tg_launch(fn, grid, block, lds_bytes, args, n_args, stream, 0);
+  }
+  OrderTable& t = order_table();
+  // held across wait, launch and record, so two host threads cannot both
+  // launch after the same recorded end
+  std::lock_guard<std::mutex> lock(t.mu);
+  OrderState& st = t.keys[std::make_pair(order_key, device)];
+  if (!st.done) TG_HIP(hipEventCreateWithFlags(&st.done, hipEventDisableTiming), "hipEventCreate");
+  if (st.pending && st.last != s)
+    TG_HIP(hipStreamWaitEvent(s, st.done, 0), "hipStreamWaitEvent");
+  const int rc = tg_launch(fn, grid, block, lds_bytes, args, n_args, stream, 0);
+  if (rc != 0) return rc;
+  TG_HIP(hipEventRecord(st.done, s), "hipEventRecord");
+  st.last = s;
+  st.pending = true;
   if (sync) TG_HIP(s ? hipStreamSynchronize(s) : hipDeviceSynchronize(), "synchronize");
   return 0;
 }

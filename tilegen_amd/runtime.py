@@ -82,6 +82,9 @@ def _declare(L) -> None:
         "tg_function_attrs": (ctypes.c_int, [_vp, _c_int_p, _c_int_p, _c_int_p, _c_int_p]),
         "tg_launch": (ctypes.c_int, [_vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                      _c_u64_p, ctypes.c_int, _vp, ctypes.c_int]),
+        "tg_launch_ordered": (ctypes.c_int, [_vp, _vp, ctypes.c_int64, ctypes.c_int32,
+                                             ctypes.c_int32, _c_u64_p, ctypes.c_int, _vp,
+                                             ctypes.c_int]),
         "tg_time_launches": (ctypes.c_int, [_vp, ctypes.c_int64, ctypes.c_int32,
                                             ctypes.c_int32, _c_u64_p, ctypes.c_int,
                                             ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp,
@@ -226,6 +229,22 @@ class DeviceBuffer:
             self.free()
         except Exception:
             pass
+
+
+def stream_create() -> int:
+    """A new non-blocking stream at the default priority (free with
+    ``stream_destroy``)."""
+    s = ctypes.c_void_p()
+    check(lib().tg_stream_create(ctypes.byref(s)), "tg_stream_create")
+    return int(s.value)
+
+
+def stream_destroy(stream: int) -> None:
+    check(lib().tg_stream_destroy(stream), "tg_stream_destroy")
+
+
+def stream_synchronize(stream: int) -> None:
+    check(lib().tg_stream_synchronize(stream), "tg_stream_synchronize")
 
 
 def pack_args(values: Sequence) -> List[int]:

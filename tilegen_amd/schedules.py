@@ -76,6 +76,15 @@ TEST_SCHEDULES: List[Config] = [
 
 TEST_KERNELS = ["spmv", "spmm", "sddmm", "fused_spmv_axpy", "axpy"]
 
+# Block sizes of 3, 5 and 7 waves: lane-group counts (3, 40, 28, 96) that are
+# not powers of two, for every combine across lane groups or waves.
+ODD_BLOCK_SCHEDULES: List[Config] = [
+    Config(tile_size=12, threads_per_row=64, unroll=1, vector_width=1, block_size=192),
+    Config(tile_size=40, threads_per_row=8, unroll=2, vector_width=2, block_size=320),
+    Config(tile_size=28, threads_per_row=16, unroll=4, vector_width=2, block_size=448),
+    Config(tile_size=96, threads_per_row=2, unroll=2, vector_width=1, block_size=192),
+]
+
 # Swept by the GPU parity tests of the merge-path (balance "nnz") SpMV and
 # fused_spmv_axpy: one wave (both window searches in one wave) and sixteen,
 # windows of about 2 to 256 rows, every lane-group width tier.

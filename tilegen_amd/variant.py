@@ -55,6 +55,7 @@ class Variant:
             ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int32),
             ctypes.POINTER(ctypes.c_int32)]
         self.lib.tgv_geometry.restype = ctypes.c_int
+        self._async = None
 
     # -- launch geometry / raw function (for timing harnesses) ------------ #
     def function(self) -> int:
@@ -108,6 +109,20 @@ class Variant:
         _rt.lib().tg_clear_error()
         self.launch(*conv)
         _rt.check_status("launch_%s" % self.kernel_name)
+
+    def launch_async(self, values: Sequence, stream: Optional[int]) -> None:
+        """Enqueue the kernel on ``stream`` (a tg_stream_create handle; None =
+        the null stream) through the library's ``tgv_launch_async``, without
+        waiting for it."""
+        if self._async is None:
+            fn = self.lib.tgv_launch_async
+            fn.argtypes = [ctypes.c_void_p] + list(_SIGNATURES[self.kernel_name])
+            fn.restype = ctypes.c_int
+            self._async = fn
+        conv = []
+        for v, t in zip(values, self.launch.argtypes):
+            conv.append(ctypes.cast(v.ptr, t) if isinstance(v, _rt.DeviceBuffer) else v)
+        _rt.check(self._async(stream, *conv), "tgv_launch_async")
 
     def run(self, A: Optional[sp.csr_matrix], out: Optional[np.ndarray] = None,
             check_structure: bool = True, **operands) -> np.ndarray:
