@@ -1,20 +1,27 @@
 #!/usr/bin/env python3
 """Benchmark of the TileGen HIP CSR hot path on one MI355X; prints ONE JSON line.
 
-A step is one launch of the case's tuned HIP variant over one copy of the
-case's inputs, already resident in HBM.  Launches rotate over enough input
-copies (>= 640 MB in total, more than the 256 MB Infinity Cache) that every
-step reads its matrix from HBM, not from a cache a previous step warmed.
+A step is one launch of a case's tuned HIP variant over one copy of the case's
+inputs, already resident in HBM.  Launches rotate over enough input copies
+(>= 640 MB in total, more than the 256 MB Infinity Cache) that every step reads
+its matrix from HBM, not from a cache a previous step warmed.
 
-value        whole-job throughput: compulsory bytes of K steps / host wall time
-             of the K steps, bracketed by device synchronizations (launch gaps
+With no ``--case`` the run covers every BASELINE config: c1 (the config the
+headline metric is quoted on) gives the top-level keys, and ``cases`` holds one
+compact entry per other config (c2, c3a, c3b, c4, c5, c5x25), each measured the
+same way in the same process.  ``--case X`` runs config X alone with full
+detail (the form the rocprofv3 commands under profiles/ use).
+
+value        headline case: compulsory bytes of K steps / host wall time of the
+             K steps, bracketed by device synchronizations (launch gaps
              included)
 roofline     per-kernel duration from start/stop events attached to each
              dispatch (hipExtModuleLaunchKernel), averaged over the timed
              launches; achieved = compulsory bytes per launch / that duration,
-             against MI355X's 8 TB/s HBM peak; traffic = HBM bytes per launch
-             measured with rocprofv3 FETCH_SIZE/WRITE_SIZE (profiles/), when a
-             summary for this kernel and case is committed
+             against MI355X's 8 TB/s HBM peak; traffic = bytes moved beyond L2
+             per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, each scaled by a
+             plain copy of known size; Infinity Cache hits count as beyond L2),
+             when a summary for this kernel and case is committed in profiles/
 cpu_baseline the reference's own sequential cpp/src/ref.cpp (oracle/_ref, kind
              "reference"; else this repository's C restatement, kind "port"),
              one host core, on the full case matrix for a bounded number of calls
@@ -24,11 +31,12 @@ cpu_openmp   this build's OpenMP CPU backend (the reference's ``_cpu_emit``
              on every OpenMP thread, host perf_counter around each call
 cpu_openmp_tuned
              the same backend at the case's CPU-tuned schedule
-             (tilegen_amd.schedules.CPU_TUNED, from tilegen_amd.cpu_tuned);
-             null for a case without one
-
-Cases are BASELINE.json's configs (tilegen_amd.matrices.baseline_ids()); the
-default c1 is the config the headline metric is quoted on.
+             (tilegen_amd.schedules.CPU_TUNED, from tilegen_amd.cpu_tuned)
+cases        per other config: us (event-timed kernel average), gbs
+             (compulsory GB/s), frac (gbs / 8000), gflops, traffic (beyond-L2
+             bytes / compulsory bytes, committed PMC summary), err (normwise
+             relative error against float64 SciPy), cpu_ms (ref.cpp, one core),
+             omp_ms / omp_tuned_ms (OpenMP backend medians, every host thread)
 """
 
 from __future__ import annotations
@@ -47,6 +55,8 @@ sys.path.insert(0, ROOT)
 METRIC = "SpMV achieved HBM GB/s (% of peak) + GFLOP/s, fp64 CSR; SpMM/SDDMM GFLOP/s"
 PEAK_HBM_GBS = 8000.0
 ROTATE_BYTES = 640 << 20
+HEADLINE = "c1"
+OTHER_CASES = ("c2", "c3a", "c3b", "c4", "c5", "c5x25")
 
 
 def _log(msg: str) -> None:
@@ -71,14 +81,19 @@ def _parse_config(text: str):
     return Config(**vals)
 
 
-def _traffic(kernel: str, case_id: str):
-    """HBM bytes per launch from a committed rocprofv3 PMC summary, or None."""
+def _pmc_summary(kernel: str, case_id: str):
     path = os.path.join(ROOT, "profiles", "%s_%s_pmc.json" % (kernel, case_id))
     if not os.path.exists(path):
         return None
     with open(path) as fh:
-        d = json.load(fh)
-    return d.get("hbm_bytes_per_launch")
+        return json.load(fh)
+
+
+def _traffic(kernel: str, case_id: str):
+    """Bytes moved beyond L2 per launch (FETCH_SIZE + WRITE_SIZE) from a
+    committed rocprofv3 PMC summary, or None."""
+    d = _pmc_summary(kernel, case_id)
+    return None if d is None else d.get("beyond_l2_bytes_per_launch")
 
 
 _COPY_SRC = r"""
@@ -118,7 +133,6 @@ def calibrate_copy(mib: int, launches: int = 10) -> int:
 def _cpu_baseline(kernel, A, ops, budget_s: float):
     import oracle
     kind = "reference" if oracle.reference_available() else "port"
-    M, N = A.shape
     if kind == "reference":
         rm = oracle.RefMatrix(A)
         K = ops[next(iter(ops))].shape[1] if kernel != "spmv" else 0
@@ -157,22 +171,181 @@ def _openmp_baseline(kernel, A, ops, K, ref, nbytes, nflop, budget_s: float, cfg
     cfg = cfg or BASELINE
     workdir = os.path.join(ROOT, "build", "bench_cpu")
     gen = generate(standard_kernels()[kernel], cfg, "cpu", outdir=workdir)
-    so, log = compile_generated(gen, "cpu", workdir)
+    so, build_log = compile_generated(gen, "cpu", workdir)
     data = (ops.get("x"), None, ops.get("B"), ops.get("U"), ops.get("V"), 1.0, 0.0)
     caller, _out, _keep = _make_caller(so, kernel, A, data, K, "cpu")
     t0 = time.perf_counter()
     got = np.asarray(caller(), dtype=np.float64).reshape(np.shape(ref))
     t1 = time.perf_counter() - t0
     err = float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-300))
+    if not err <= 1e-10:
+        raise SystemExit("OpenMP backend check failed for %s: rel err %.3e" % (kernel, err))
     iters = int(max(5, min(2000, budget_s / max(t1, 1e-6))))
     ms = _time_host(caller.launch, 2, iters)
     med = float(np.median(ms)) * 1e-3
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": _omp_threads(),
             "kind": "openmp backend", "schedule": cfg.short(),
-            "sample": "%d calls of the full matrix, median %.3f ms per call" % (iters, med * 1e3),
             "gflops": round(nflop / med / 1e9, 3), "ms_median": round(med * 1e3, 4),
-            "ms_min": round(float(np.min(ms)), 4), "rel_err": err,
-            "compile": log.split(" with: ")[-1]}
+            "calls": iters, "rel_err": err, "compile": build_log.split(" with: ")[-1]}
+
+
+def _scipy_reference(kernel, A, ops):
+    """float64 SciPy/numpy result of the case (the check of this run)."""
+    if kernel == "spmv":
+        return A @ ops["x"]
+    if kernel == "spmm":
+        return A @ ops["B"]
+    coo = A.tocoo()
+    out = np.empty(coo.nnz)
+    step = 1 << 21
+    for s in range(0, coo.nnz, step):
+        e = min(s + step, coo.nnz)
+        out[s:e] = np.einsum("ik,ik->i", ops["U"][coo.row[s:e]], ops["V"][coo.col[s:e]]) \
+            * coo.data[s:e]
+    return out
+
+
+class CaseRun:
+    """One BASELINE config resident on the device: its tuned variant, rotated
+    input copies and the argument sets that launch over them."""
+
+    def __init__(self, case_id: str, cfg, warm: bool):
+        from tilegen_amd import runtime as rt
+        from tilegen_amd.matrices import (baseline_case, baseline_operands, compulsory_bytes,
+                                          flops, make_baseline)
+        from tilegen_amd.variant import Variant
+        t0 = time.time()
+        self.case_id = case_id
+        self.case = baseline_case(case_id)
+        self.kernel = self.case.kernel
+        self.cfg = cfg
+        self.A = make_baseline(case_id)
+        self.M, self.N = self.A.shape
+        self.nnz = int(self.A.nnz)
+        self.K = self.case.K
+        self.ops = baseline_operands(self.kernel, self.M, self.N, self.K)
+        self.v = Variant(self.kernel, cfg)
+        self.fn = self.v.function()
+        self.grid, self.block, self.lds = self.v.geometry(self.M, self.N, self.K, self.nnz)
+        self.nbytes = compulsory_bytes(self.kernel, self.M, self.N, self.nnz, self.K)
+        self.nflop = flops(self.kernel, self.nnz, self.K)
+        self.copies = 1 if warm else int(min(64, max(2, -(-ROTATE_BYTES // self.nbytes))))
+        host = {"indptr": self.A.indptr.astype(np.int64),
+                "indices": self.A.indices.astype(np.int64),
+                "data": self.A.data.astype(np.float64)}
+        host.update({k: np.ascontiguousarray(val, dtype=np.float64)
+                     for k, val in self.ops.items()})
+        self.out_name = {"spmv": "y", "spmm": "C", "sddmm": "C"}[self.kernel]
+        self.out_shape = {"spmv": (self.M,), "spmm": (self.M, self.K),
+                          "sddmm": (self.nnz,)}[self.kernel]
+        self.sets, self.keep = [], []
+        for _ in range(self.copies):
+            bufs = {k: rt.DeviceBuffer(a) for k, a in host.items()}
+            bufs[self.out_name] = rt.DeviceBuffer(np.zeros(self.out_shape))
+            self.keep.append(bufs)
+            self.sets.append(self.v.abi_values(self.A, bufs, {}, self.M, self.N, self.K,
+                                               self.nnz))
+        _log("%s (%s) M=%d N=%d nnz=%d K=%d, %s grid=%d block=%d, %d copies (%.0f MB) "
+             "resident in %.1fs" % (case_id, self.kernel, self.M, self.N, self.nnz, self.K,
+                                    cfg.short(), self.grid, self.block, self.copies,
+                                    self.copies * self.nbytes / 1e6, time.time() - t0))
+
+    def check(self):
+        """One launch through the C ABI, against float64 SciPy; returns
+        (reference, normwise relative error)."""
+        self.v.device_call(self.sets[0])
+        got = self.keep[0][self.out_name].to_host()
+        ref = _scipy_reference(self.kernel, self.A, self.ops)
+        err = float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-300))
+        _log("%s check vs float64 SciPy: normwise rel err %.3e" % (self.case_id, err))
+        if not err <= 1e-10:
+            raise SystemExit("%s result check failed: rel err %.3e" % (self.case_id, err))
+        return ref, err
+
+    def time_events(self, warmup: int, iters: int):
+        from tilegen_amd import runtime as rt
+        kms, ev_wall_ms = rt.time_launches(self.fn, self.grid, self.block, self.lds, self.sets,
+                                           warmup, iters)
+        return kms, ev_wall_ms
+
+    def free(self) -> None:
+        for bufs in self.keep:
+            for b in bufs.values():
+                b.free()
+        self.keep, self.sets = [], []
+
+
+def _vendor_leg(run: CaseRun, alg: str, ref, warmup: int, steps: int):
+    from tilegen_amd import vendor as vd
+    A, ops, kernel = run.A, run.ops, run.kernel
+    M, N, K, nnz = run.M, run.N, run.K, run.nnz
+    for b in run.keep:  # the vendor call writes the same output buffers
+        b[run.out_name].upload(np.zeros(run.out_shape))
+    if kernel == "spmv":
+        vsets = [[b["indptr"], b["indices"], b["data"], b["x"], b["y"]] for b in run.keep]
+        vms, _ = vd.spmv_time(alg, M, N, nnz, vsets, warmup, steps)
+        vref, call = ref, "rocsparse_spmv compute call"
+    elif kernel == "spmm":
+        vsets = [[b["indptr"], b["indices"], b["data"], b["B"], b["C"]] for b in run.keep]
+        vms, _ = vd.spmm_time(alg, M, N, K, nnz, vsets, warmup, steps)
+        vref, call = ref, "rocsparse_spmm compute call"
+    else:
+        vsets = [[b["indptr"], b["indices"], b["U"], b["V"], b["C"]] for b in run.keep]
+        vms, _ = vd.sddmm_time(alg, M, N, K, nnz, vsets, warmup, steps)
+        # rocSPARSE's SDDMM does not multiply by A's values
+        coo = A.tocoo()
+        vref = np.einsum("ik,ik->i", ops["U"][coo.row], ops["V"][coo.col])
+        call = "rocsparse_sddmm call (no multiply by A's values)"
+    vgot = run.keep[0][run.out_name].to_host().reshape(np.shape(vref))
+    verr = float(np.abs(vgot - vref).max() / max(np.abs(vref).max(), 1e-300))
+    vmed = float(np.median(vms)) * 1e-3
+    _log("rocSPARSE %s: median %.2f us per call (%.0f GB/s, %.0f GFLOP/s), rel err %.2e" % (
+        alg, vmed * 1e6, run.nbytes / vmed / 1e9, run.nflop / vmed / 1e9, verr))
+    return {"library": "rocSPARSE", "alg": alg, "us_median": round(vmed * 1e6, 3),
+            "gbs_median": round(run.nbytes / vmed / 1e9, 2),
+            "gflops_median": round(run.nflop / vmed / 1e9, 2),
+            "timer": "hipEvents around each " + call, "rel_err": verr}
+
+
+def _cpu_legs(run: CaseRun, ref, budget_s: float):
+    """(cpu_baseline, cpu_openmp, cpu_openmp_tuned) of a case on this host."""
+    from tilegen_amd.schedules import CPU_TUNED
+    kind, sec, iters = _cpu_baseline(run.kernel, run.A, run.ops, budget_s / 2)
+    cpu = {"value": round(run.nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
+           "sample": "%d sequential calls of the full %s matrix (%d rows, %d nnz), %.3f ms "
+                     "per call" % (iters, run.case_id, run.M, run.nnz, sec * 1e3),
+           "gflops": round(run.nflop / sec / 1e9, 3), "ms_per_call": round(sec * 1e3, 4)}
+    _log("%s cpu baseline (%s): %.3f ms per call" % (run.case_id, kind, sec * 1e3))
+    omp = _openmp_baseline(run.kernel, run.A, run.ops, run.K, ref, run.nbytes, run.nflop,
+                           budget_s / 4)
+    _log("%s cpu OpenMP backend (%d threads): median %.3f ms" % (run.case_id, omp["cores"],
+                                                                omp["ms_median"]))
+    omp_tuned = None
+    if run.case_id in CPU_TUNED:
+        omp_tuned = _openmp_baseline(run.kernel, run.A, run.ops, run.K, ref, run.nbytes,
+                                     run.nflop, budget_s / 4, CPU_TUNED[run.case_id])
+        omp_tuned["kind"] = "openmp backend, CPU-tuned schedule"
+        _log("%s cpu OpenMP backend, tuned %s: median %.3f ms" % (
+            run.case_id, omp_tuned["schedule"], omp_tuned["ms_median"]))
+    return cpu, omp, omp_tuned
+
+
+def _case_entry(run: CaseRun, kms, err, cpu, omp, omp_tuned):
+    """The compact per-config record of ``cases``."""
+    avg = float(kms.mean()) * 1e-3
+    gbs = run.nbytes / avg / 1e9
+    traffic = _traffic(run.kernel, run.case_id)
+    return {
+        "kernel": run.kernel, "sched": run.cfg.short(), "nnz": run.nnz,
+        "us": round(avg * 1e6, 3), "us_med": round(float(np.median(kms)) * 1e3, 3),
+        "gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
+        "gflops": round(run.nflop / avg / 1e9, 1),
+        "traffic": round(traffic / run.nbytes, 3) if traffic else None,
+        "err": float("%.3g" % err),
+        "cpu_ms": cpu["ms_per_call"] if cpu else None,
+        "omp_ms": omp["ms_median"] if omp else None,
+        "omp_tuned_ms": omp_tuned["ms_median"] if omp_tuned else None,
+    }
 
 
 def main(argv=None) -> int:
@@ -180,13 +353,20 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--case", default="c1")
+    ap.add_argument("--case", default=None,
+                    help="run this BASELINE config alone (default: c1 as the headline plus "
+                         "every other config under 'cases')")
     ap.add_argument("--config", default=None,
-                    help="schedule override, e.g. T128/TPR8/U2/V1/B256 (append /nnz for "
-                         "merge-path windows, /hybrid for long-row workgroups)")
+                    help="schedule override for the headline case, e.g. T128/TPR8/U2/V1/B256 "
+                         "(append /nnz for merge-path windows, /hybrid for long-row "
+                         "workgroups)")
+    ap.add_argument("--case-iters", type=int, default=200,
+                    help="event-timed launches per config under 'cases'")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="bound on the CPU baseline's timed calls")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+                    help="bound on the headline case's CPU legs")
+    ap.add_argument("--case-cpu-seconds", type=float, default=3.0,
+                    help="bound on each other config's CPU legs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU legs")
     ap.add_argument("--warm", action="store_true",
                     help="no input rotation (cache-warm figure, reported as such)")
     ap.add_argument("--vendor", default=None, metavar="ALG",
@@ -206,144 +386,47 @@ def main(argv=None) -> int:
         return calibrate_copy(args.calibrate_copy)
 
     from tilegen_amd import runtime as rt
-    from tilegen_amd.matrices import (baseline_case, baseline_operands, compulsory_bytes,
-                                      flops, make_baseline)
     from tilegen_amd.schedules import TUNED
-    from tilegen_amd.variant import Variant
 
-    case = baseline_case(args.case)
-    cfg = _parse_config(args.config) if args.config else TUNED[args.case]
-    t_gen = time.time()
-    A = make_baseline(args.case)
-    M, N = A.shape
-    nnz = int(A.nnz)
-    K = case.K
-    ops = baseline_operands(case.kernel, M, N, K)
-    _log("case %s (%s) M=%d N=%d nnz=%d K=%d generated in %.1fs" % (
-        args.case, case.kernel, M, N, nnz, K, time.time() - t_gen))
-
+    head_id = args.case or HEADLINE
+    others = [] if args.case else list(OTHER_CASES)
     if rt.device_count() < 1:
         raise SystemExit("no HIP device visible")
     dev = rt.device_info(0)
-    v = Variant(case.kernel, cfg)
-    fn = v.function()
-    grid, block, lds = v.geometry(M, N, K, nnz)
-    attrs = v.attrs()
-    _log("device %s (%s, %d CUs); variant %s grid=%d block=%d lds=%d %s" % (
-        dev["name"], dev["arch"], dev["cu_count"], cfg.short(), grid, block, lds, attrs))
+    cfg = _parse_config(args.config) if args.config else TUNED[head_id]
+    run = CaseRun(head_id, cfg, args.warm)
+    _log("device %s (%s, %d CUs); variant attrs %s" % (dev["name"], dev["arch"],
+                                                       dev["cu_count"], run.v.attrs()))
+    ref, err = run.check()
 
-    nbytes = compulsory_bytes(case.kernel, M, N, nnz, K)
-    nflop = flops(case.kernel, nnz, K)
-    copies = 1 if args.warm else int(min(64, max(2, -(-ROTATE_BYTES // nbytes))))
-
-    host = {"indptr": A.indptr.astype(np.int64), "indices": A.indices.astype(np.int64),
-            "data": A.data.astype(np.float64)}
-    host.update({k: np.ascontiguousarray(val, dtype=np.float64) for k, val in ops.items()})
-    out_name = {"spmv": "y", "spmm": "C", "sddmm": "C"}[case.kernel]
-    out_shape = {"spmv": (M,), "spmm": (M, K), "sddmm": (nnz,)}[case.kernel]
-    sets, keep = [], []
-    for c in range(copies):
-        bufs = {k: rt.DeviceBuffer(a) for k, a in host.items()}
-        bufs[out_name] = rt.DeviceBuffer(np.zeros(out_shape))
-        keep.append(bufs)
-        sets.append(v.abi_values(A, bufs, {}, M, N, K, nnz))
-    _log("%d input copies resident (%.0f MB)" % (copies, copies * nbytes / 1e6))
-
-    # one checked launch through the C ABI before timing
-    v.device_call(sets[0])
-    got = keep[0][out_name].to_host()
-    import scipy.sparse  # noqa: F401  (float64 check of this run, not the oracle)
-    if case.kernel == "spmv":
-        ref = A @ ops["x"]
-    elif case.kernel == "spmm":
-        ref = A @ ops["B"]
-    else:
-        coo = A.tocoo()
-        ref = np.einsum("ik,ik->i", ops["U"][coo.row], ops["V"][coo.col]) * coo.data
-    err = float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-300))
-    _log("check vs float64 SciPy: normwise rel err %.3e" % err)
-    if not err <= 1e-10:
-        raise SystemExit("result check failed: rel err %.3e" % err)
-
-    arg_sets = rt.ArgSets(sets)
-    rt.run_launches(fn, grid, block, lds, arg_sets, args.warmup)
+    arg_sets = rt.ArgSets(run.sets)
+    rt.run_launches(run.fn, run.grid, run.block, run.lds, arg_sets, args.warmup)
     rt.synchronize()
     t0 = time.perf_counter()
-    rt.run_launches(fn, grid, block, lds, arg_sets, args.steps)
+    rt.run_launches(run.fn, run.grid, run.block, run.lds, arg_sets, args.steps)
     rt.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall / args.steps * 1e3
-    value = nbytes * args.steps / wall / 1e9
+    value = run.nbytes * args.steps / wall / 1e9
 
-    kms, ev_wall_ms = rt.time_launches(fn, grid, block, lds, sets, args.warmup, args.steps)
+    kms, ev_wall_ms = run.time_events(args.warmup, args.steps)
     k_avg_s = float(kms.mean()) * 1e-3
     k_med_s = float(np.median(kms)) * 1e-3
-    achieved = nbytes / k_avg_s / 1e9
-    _log("timed %d steps: %.3f ms/step (host clock), kernel avg %.2f us median %.2f us, "
-         "events wall %.3f ms/step" % (args.steps, ms_per_step, k_avg_s * 1e6, k_med_s * 1e6,
-                                        ev_wall_ms / args.steps))
+    achieved = run.nbytes / k_avg_s / 1e9
+    _log("%s timed %d steps: %.3f ms/step (host clock), kernel avg %.2f us median %.2f us, "
+         "events wall %.3f ms/step" % (head_id, args.steps, ms_per_step, k_avg_s * 1e6,
+                                        k_med_s * 1e6, ev_wall_ms / args.steps))
 
-    vendor = None
-    if args.vendor:
-        from tilegen_amd import vendor as vd
-        out_key = {"spmv": "y", "spmm": "C", "sddmm": "C"}[case.kernel]
-        for b in keep:  # the vendor call writes the same output buffers
-            b[out_key].upload(np.zeros(out_shape))
-        if case.kernel == "spmv":
-            vsets = [[b["indptr"], b["indices"], b["data"], b["x"], b["y"]] for b in keep]
-            vms, _ = vd.spmv_time(args.vendor, M, N, nnz, vsets, args.warmup, args.steps)
-            vref, call = ref, "rocsparse_spmv compute call"
-        elif case.kernel == "spmm":
-            vsets = [[b["indptr"], b["indices"], b["data"], b["B"], b["C"]] for b in keep]
-            vms, _ = vd.spmm_time(args.vendor, M, N, K, nnz, vsets, args.warmup, args.steps)
-            vref, call = ref, "rocsparse_spmm compute call"
-        else:
-            vsets = [[b["indptr"], b["indices"], b["U"], b["V"], b["C"]] for b in keep]
-            vms, _ = vd.sddmm_time(args.vendor, M, N, K, nnz, vsets, args.warmup, args.steps)
-            # rocSPARSE's SDDMM does not multiply by A's values
-            coo = A.tocoo()
-            vref = np.einsum("ik,ik->i", ops["U"][coo.row], ops["V"][coo.col])
-            call = "rocsparse_sddmm call (no multiply by A's values)"
-        vgot = keep[0][out_key].to_host().reshape(np.shape(vref))
-        verr = float(np.abs(vgot - vref).max() / max(np.abs(vref).max(), 1e-300))
-        vmed = float(np.median(vms)) * 1e-3
-        vendor = {"library": "rocSPARSE", "alg": args.vendor, "us_median": round(vmed * 1e6, 3),
-                  "gbs_median": round(nbytes / vmed / 1e9, 2),
-                  "gflops_median": round(nflop / vmed / 1e9, 2),
-                  "timer": "hipEvents around each " + call, "rel_err": verr}
-        _log("rocSPARSE %s: median %.2f us per call (%.0f GB/s, %.0f GFLOP/s), rel err %.2e" % (
-            args.vendor, vmed * 1e6, nbytes / vmed / 1e9, nflop / vmed / 1e9, verr))
-
-    cpu = None
+    vendor = _vendor_leg(run, args.vendor, ref, args.warmup, args.steps) if args.vendor else None
+    cpu = omp = omp_tuned = None
     if not args.no_cpu:
-        kind, sec, iters = _cpu_baseline(case.kernel, A, ops, args.cpu_seconds)
-        cpu = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
-               "sample": "%d sequential calls of the full %s matrix (%d rows, %d nnz), "
-                         "%.3f ms per call" % (iters, args.case, M, nnz, sec * 1e3),
-               "gflops": round(nflop / sec / 1e9, 3), "ms_per_call": round(sec * 1e3, 4)}
-        _log("cpu baseline (%s): %.3f ms per call" % (kind, sec * 1e3))
+        cpu, omp, omp_tuned = _cpu_legs(run, ref, args.cpu_seconds)
+    run.free()
 
-    omp = omp_tuned = None
-    if not args.no_cpu:
-        omp = _openmp_baseline(case.kernel, A, ops, K, ref, nbytes, nflop, args.cpu_seconds / 2)
-        _log("cpu OpenMP backend (%d threads): %s" % (omp["cores"], omp["sample"]))
-        from tilegen_amd.schedules import CPU_TUNED
-        if args.case in CPU_TUNED:
-            omp_tuned = _openmp_baseline(case.kernel, A, ops, K, ref, nbytes, nflop,
-                                         args.cpu_seconds / 2, CPU_TUNED[args.case])
-            omp_tuned["kind"] = "openmp backend, CPU-tuned schedule"
-            _log("cpu OpenMP backend, tuned %s: %s" % (omp_tuned["schedule"],
-                                                      omp_tuned["sample"]))
-
-    for bufs in keep:
-        for b in bufs.values():
-            b.free()
-
-    unit = "GB/s"
     line = {
         "metric": METRIC,
         "value": round(value, 2),
-        "unit": unit,
+        "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -354,34 +437,50 @@ def main(argv=None) -> int:
         "dtype": "f64",
         "data": "synthetic (seeded BASELINE config generator, U(-1,1) values)",
         "config": {
-            "workload": "%s: %s" % (args.case, case.description),
-            "case": args.case, "kernel": case.kernel, "rows": M, "cols": N, "nnz": nnz,
-            "K": K, "schedule": cfg.short(), "grid": grid, "block": block,
-            "input_copies": copies, "cache": "warm" if args.warm else "cold (rotated)",
-            "compulsory_bytes": nbytes,
+            "workload": "%s: %s" % (head_id, run.case.description),
+            "case": head_id, "kernel": run.kernel, "rows": run.M, "cols": run.N,
+            "nnz": run.nnz, "K": run.K, "schedule": cfg.short(), "grid": run.grid,
+            "block": run.block, "input_copies": run.copies,
+            "cache": "warm" if args.warm else "cold (rotated)",
+            "compulsory_bytes": run.nbytes,
         },
-        "gflops": round(nflop * args.steps / wall / 1e9, 3),
+        "gflops": round(run.nflop * args.steps / wall / 1e9, 3),
         "pct_of_peak_hbm": round(100.0 * value / PEAK_HBM_GBS, 2),
         "kernel_us_avg": round(k_avg_s * 1e6, 3),
         "kernel_us_median": round(k_med_s * 1e6, 3),
-        "kernel_gbs_median": round(nbytes / k_med_s / 1e9, 2),
-        "kernel_gflops_avg": round(nflop / k_avg_s / 1e9, 3),
+        "kernel_gflops_avg": round(run.nflop / k_avg_s / 1e9, 3),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": _traffic(case.kernel, args.case),
+            "traffic": _traffic(run.kernel, head_id),
         },
         "cpu_baseline": cpu,
         "cpu_openmp": omp,
         "cpu_openmp_tuned": omp_tuned,
-        "vendor": vendor,
         "check_rel_err": err,
-        "device": "%s %s" % (dev["name"], dev["arch"]),
     }
-    print(json.dumps(line), flush=True)
+    if vendor is not None:
+        line["vendor"] = vendor
+
+    if others:
+        cases = {}
+        for cid in others:
+            crun = CaseRun(cid, TUNED[cid], args.warm)
+            cref, cerr = crun.check()
+            ckms, _ = crun.time_events(args.warmup, args.case_iters)
+            _log("%s kernel avg %.2f us median %.2f us over %d launches" % (
+                cid, float(ckms.mean()) * 1e3, float(np.median(ckms)) * 1e3, args.case_iters))
+            ccpu = comp = comp_t = None
+            if not args.no_cpu:
+                ccpu, comp, comp_t = _cpu_legs(crun, cref, args.case_cpu_seconds)
+            crun.free()
+            cases[cid] = _case_entry(crun, ckms, cerr, ccpu, comp, comp_t)
+        line["cases"] = cases
+    line["device"] = dev["arch"].split(":")[0]
+    print(json.dumps(line, separators=(",", ":")), flush=True)
     return 0
 
 

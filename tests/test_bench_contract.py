@@ -39,12 +39,21 @@ def test_config_parser_and_traffic_lookup():
 
 
 @pytest.mark.gpu
+@pytest.mark.timeout(500)
 def test_bench_json_line(hip_ready):
-    r = _bench("--steps", "20", "--warmup", "2", "--cpu-seconds", "1")
+    """The default run: c1 as the headline plus every other BASELINE config."""
+    r = _bench("--steps", "20", "--warmup", "2", "--cpu-seconds", "1", "--case-cpu-seconds",
+               "0.3", "--case-iters", "10", timeout=480)
     assert r.returncode == 0, r.stderr[-2000:]
     lines = [l for l in r.stdout.splitlines() if l.strip()]
     assert len(lines) == 1
+    assert len(lines[0]) < 3600, len(lines[0])  # a driver's tail holds it whole
     out = json.loads(lines[0])
+    assert sorted(out["cases"]) == sorted(["c2", "c3a", "c3b", "c4", "c5", "c5x25"])
+    for cid, c in out["cases"].items():
+        assert c["err"] <= 1e-10 and c["us"] > 0 and c["gflops"] > 0, cid
+        assert abs(c["frac"] - c["gbs"] / 8000.0) < 1e-3, cid
+        assert c["cpu_ms"] > 0 and c["omp_ms"] > 0, cid
     for k in KEYS:
         assert k in out, k
     assert out["n_gpus"] == 1 and out["steps"] == 20 and out["unit"] == "GB/s"
