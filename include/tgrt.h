@@ -33,6 +33,9 @@ typedef void* tg_function;
 const char* tg_last_error(void);
 int tg_last_status(void);
 void tg_clear_error(void);
+/* Records `code` and `message` for tg_last_status/tg_last_error on the calling
+ * thread and returns `code`: how libraries layered on libtgrt report. */
+int tg_fail(int code, const char* message);
 
 /* ---- devices (replaces env.py:55-83 `_gpu_info` for the HIP backend) ---- */
 int tg_device_count(int* count);

@@ -206,7 +206,7 @@ def test_merge_source_and_refusals():
     for k in ("spmv", "fused_spmv_axpy"):
         g = cg.generate(ks[k], cfg, backend="hip", write=False)
         assert "tg_mp_search(indptr, row_lim, t0, X, 1)" in g.source
-        assert "tg_mp_commit(wdx, wf, wl, t, &tot)" in g.source
+        assert "tg_mp_commit(tg_part, wdx, wf, wl, t, &tot)" in g.source
         tiling = [e for e in cg._passes.run_pipeline(ks[k], cfg, backend="hip").pass_log
                   if e["pass"] == "tiling"][0]
         assert "merge path" in tiling["action"]

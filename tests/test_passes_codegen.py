@@ -416,3 +416,38 @@ def test_scratch_modules_launch_in_order(balance, ordered):
         assert ("tg_launch_ordered(tg_code, fn," in async_fn) == ordered
         assert ("return tg_launch(fn," in async_fn) == (not ordered)
         assert ("tg_mp_part" in emit_hip(k, cfg)) == ordered
+
+
+def test_scratch_argument_form_of_scratch_modules():
+    """scratch_arg: the same kernel with its slots as a last parameter and no
+    module array; refused for variants that combine nothing."""
+    cfg = Config(tile_size=64, threads_per_row=4, unroll=4, block_size=256, balance="hybrid")
+    k = _run(standard_kernels()["spmv"], cfg, "hip")
+    mod, arg = emit_hip(k, cfg), emit_hip(k, cfg, scratch_arg=True)
+    assert "__device__ unsigned long long tg_mp_part[" in mod
+    assert "tg_mp_part" not in arg
+    assert "unsigned long long* __restrict__ tg_part)" in arg
+    assert "unsigned long long* const tg_part = tg_mp_part;" in mod
+
+    def code(t):  # the lines that do not name where the slots come from
+        t = t.replace(", unsigned long long* __restrict__ tg_part)", ")")
+        return [l for l in t.splitlines()
+                if "tg_mp_part" not in l and not l.lstrip().startswith("//")]
+    assert code(mod) == code(arg)
+    rows = Config(tile_size=64, threads_per_row=4)
+    with pytest.raises(ValueError, match="scratch_arg"):
+        emit_hip(_run(standard_kernels()["spmv"], rows, "hip"), rows, scratch_arg=True)
+
+
+def test_noalloc_kernel_source_geometry():
+    from tilegen_amd.build import NOALLOC_CASE, noalloc_kernel_source
+    from tilegen_amd.codegen import MERGE_CAP, hybrid_chunk
+    from tilegen_amd.schedules import TUNED
+    src = noalloc_kernel_source()
+    cfg = TUNED[NOALLOC_CASE]
+    chunk = 2 * cfg.block_size * cfg.unroll
+    assert "#define TG_NA_CHUNK %d " % chunk in src
+    assert "#define TG_NA_SLOTS %d " % (2 * MERGE_CAP) in src
+    assert "#define TG_NA_MAX_NNZ %dLL" % (MERGE_CAP * chunk) in src
+    assert "#define TG_NA_BLOCK %d" % cfg.block_size in src
+    assert "__device__ unsigned long long tg_mp_part[" not in src

@@ -778,8 +778,10 @@ def _tile_stats(w: _W, TR: int) -> None:
 MERGE_CAP = 65536
 
 
-def _merge_decls(pre: _W) -> None:
-    """File-scope search, scratch and combine of the merge-path SpMV."""
+def _merge_decls(pre: _W, scratch_arg: bool = False) -> None:
+    """File-scope search, scratch and combine of the merge-path SpMV.  With
+    ``scratch_arg`` the kernel takes its scratch as a parameter instead of the
+    module-scope array."""
     pre(r"""// Merge path: row r occupies items r + indptr[r] .. r + indptr[r + 1] (its
 // nonzeros, then one item that ends it); the launch's items are cut into one
 // window per workgroup.
@@ -826,10 +828,9 @@ __device__ tg_i64 tg_mp_search(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i
 // before it (slot 2w).  A slot holds 0 when empty and bits(partial) ^ TG_MP_KEY
 // when full; TG_MP_KEY is a signalling-NaN pattern, which no floating-point
 // sum produces, so a full slot is never 0.  Only device-scope atomics touch the
-// slots.  Two launches of this module must not overlap on one device: the host
-// launcher orders each launch after the previous one (tg_launch_ordered).
+// slots.  Two launches that share the slots must not overlap on one device.
 #define TG_MP_KEY 0x7FF4A5A5A5A5A5A5ull
-__device__ unsigned long long tg_mp_part[%(P)d];
+%(DECL)s
 
 // The value must be in a register (so the atomic that produced it has returned)
 // before any later memory operation is issued.
@@ -846,11 +847,12 @@ __device__ __forceinline__ void tg_mp_wait(unsigned long long v) {
 // reduction tree, empties them and returns true with the sum in *tot; pieces
 // that find an empty slot return false.  Every combiner computes the same bits,
 // every slot is empty again when the launch ends, and no wave waits for another.
-__device__ bool tg_mp_commit(tg_i64 w, tg_i64 wf, tg_i64 wl, double t, double* tot) {
+__device__ bool tg_mp_commit(unsigned long long* __restrict__ part, tg_i64 w, tg_i64 wf,
+                             tg_i64 wl, double t, double* tot) {
   const int l = threadIdx.x & 63;
   unsigned long long mine = 0;
   if (l == 0)
-    mine = __hip_atomic_exchange(tg_mp_part + 2 * w + (w == wf ? 1 : 0),
+    mine = __hip_atomic_exchange(part + 2 * w + (w == wf ? 1 : 0),
                                  (unsigned long long)__double_as_longlong(t) ^ TG_MP_KEY,
                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   tg_mp_wait(__shfl((long long)mine, 0));
@@ -863,7 +865,7 @@ __device__ bool tg_mp_commit(tg_i64 w, tg_i64 wf, tg_i64 wl, double t, double* t
       // a compare-and-swap that never matches (no slot holds 1) reads the slot where
       // the swaps are performed; an idempotent add or or may be turned into a load
       b = 1ull;
-      __hip_atomic_compare_exchange_strong(tg_mp_part + 2 * v + (v == wf ? 1 : 0), &b, 1ull,
+      __hip_atomic_compare_exchange_strong(part + 2 * v + (v == wf ? 1 : 0), &b, 1ull,
                                            __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -874,13 +876,17 @@ __device__ bool tg_mp_commit(tg_i64 w, tg_i64 wf, tg_i64 wl, double t, double* t
   for (tg_i64 base = wf; base <= wl; base += 64) {
     const tg_i64 v = base + l;
     if (v <= wl)
-      (void)__hip_atomic_exchange(tg_mp_part + 2 * v + (v == wf ? 1 : 0), 0ull,
+      (void)__hip_atomic_exchange(part + 2 * v + (v == wf ? 1 : 0), 0ull,
                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   *tot = sum;
   return true;
 }
-""" % {"P": 2 * MERGE_CAP})
+""" % {"DECL": ("// the slots arrive as the kernel's last parameter, tg_part (%d of them)"
+                  % (2 * MERGE_CAP)) if scratch_arg else
+          ("// module scratch: the host launcher orders each launch after the previous one\n"
+           "// on any stream (tg_launch_ordered)\n"
+           "__device__ unsigned long long tg_mp_part[%d];" % (2 * MERGE_CAP))})
 
 
 def _merge_window(w: _W, TR: int, WAVES: int) -> None:
@@ -999,7 +1005,7 @@ def _hybrid_ranges(w: _W, plan: Plan, step, out_name: str, B: int, U: int, ALIGN
     w("#pragma unroll")
     w("for (int v = 0; v < %d; ++v) t += s_hred[v];" % WAVES)
     w("double tot = t;")
-    w("const bool done = !cut || tg_mp_commit(e, ef, el, t, &tot);")
+    w("const bool done = !cut || tg_mp_commit(tg_part, e, ef, el, t, &tot);")
     w.open("if (done && threadIdx.x == 0)")
     env = _Env({row: "row"}, acc="tot")
     w("__builtin_nontemporal_store(%s, %s + %s);" % (
@@ -1013,7 +1019,8 @@ def _hybrid_ranges(w: _W, plan: Plan, step, out_name: str, B: int, U: int, ALIGN
 
 
 def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeometry,
-                       out_name: str, pre: Optional[_W] = None) -> None:
+                       out_name: str, pre: Optional[_W] = None,
+                       scratch_arg: bool = False) -> None:
     """y[row] = final(sum over the row's nonzeros of value_expr).
 
     Tiled variants also balance skewed rows without any preprocessing: a row
@@ -1094,7 +1101,9 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     if merge or hybrid:
         if pre is None:
             raise ValueError("merge-path and hybrid tiles need file-scope declarations")
-        _merge_decls(pre)
+        _merge_decls(pre, scratch_arg)
+        if not scratch_arg:
+            w("unsigned long long* const tg_part = tg_mp_part;")
     if merge:
         # a window holds about T rows' worth of items but may hold several times
         # T short rows; a batch is at least one row per lane group
@@ -1301,7 +1310,7 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w("for (int v = 0; v < %d; ++v) t += s_red[v];" % WAVES)
     w("const tg_i64 wf = (row + pb) / D, wl = (row + pe - 1) / D;  // its first/last window")
     w("double tot;")
-    w.open("if (tg_mp_commit(wdx, wf, wl, t, &tot) && threadIdx.x == 0)")
+    w.open("if (tg_mp_commit(tg_part, wdx, wf, wl, t, &tot) && threadIdx.x == 0)")
     env = _Env({row: "row"}, acc="tot")
     w("__builtin_nontemporal_store(%s, %s + %s);" % (
         _cexpr(plan.final_expr, env), out_name, _offset(plan.out_tensor, plan.out.indices, env)))
@@ -1806,18 +1815,23 @@ def _dense_name(plan: Plan, which: int) -> str:
 
 
 def _hip_kernel_text(kernel: Kernel, config: Config, plan: Plan, low: Lowering,
-                     args: List[Tuple[str, str]], geo: LaunchGeometry) -> str:
+                     args: List[Tuple[str, str]], geo: LaunchGeometry,
+                     scratch_arg: bool = False) -> str:
     bound = "(%s - 1)" % plan.row_extent if config.inject_bug else plan.row_extent
     out_name = plan.out_tensor.name
     pre = _W()  # file-scope declarations the kernel needs
     w = _W()
     w("extern \"C\" __global__ __launch_bounds__(%d)" % geo.block)
-    w.open("void %s_kernel(%s)" % (kernel.name, _hip_decls(args)))
+    params = _hip_decls(args)
+    if scratch_arg:
+        params += ", unsigned long long* __restrict__ tg_part"
+    w.open("void %s_kernel(%s)" % (kernel.name, params))
     if plan.kind == "scalar_reduce":
         if not plan.reduce_is_compressed:
             raise NotImplementedError("HIP scalar_reduce needs the reduction over the "
                                       "compressed index")
-        _hip_scalar_reduce(w, plan, low, bound, geo, out_name, pre=pre)
+        _hip_scalar_reduce(w, plan, low, bound, geo, out_name, pre=pre,
+                           scratch_arg=scratch_arg)
     elif plan.kind == "row_dense_out":
         kext = _extent_for(plan, plan.inner_out[0].name)
         _hip_row_dense_out(w, plan, low, bound, geo, out_name, _dense_name(plan, 0), kext)
@@ -1843,10 +1857,18 @@ def _check_hip_dtype(config: Config) -> None:
                          % (config.dtype, config.dtype))
 
 
-def emit_hip(kernel: Kernel, config: Config) -> str:
-    """Device translation unit of a lowered kernel (hipRTC input)."""
+def emit_hip(kernel: Kernel, config: Config, scratch_arg: bool = False) -> str:
+    """Device translation unit of a lowered kernel (hipRTC input).
+
+    ``scratch_arg`` (merge-path and hybrid variants only): the kernel takes the
+    slots it combines row pieces through as a last parameter,
+    ``unsigned long long* tg_part`` (2 * MERGE_CAP of them, all zero between
+    launches), instead of declaring them as module scratch."""
     _check_hip_dtype(config)
     plan, low = _plan(kernel), _lowering(kernel)
+    if scratch_arg and not module_scratch(plan, low):
+        raise ValueError("scratch_arg applies to merge-path and hybrid variants only; %s "
+                         "combines nothing across workgroups" % config.short())
     if config.balance != "rows" and config.tile_size <= 1:
         raise ValueError("balance '%s' needs a tile (tile_size > 1); %s is untiled"
                          % (config.balance, config.short()))
@@ -1859,7 +1881,7 @@ def emit_hip(kernel: Kernel, config: Config) -> str:
                 " + ceil(nnz / %d)" % geo.nnz_chunk if geo.nnz_chunk else "",
                 geo.block, geo.lds_bytes)]
     return "\n".join([_header(kernel, config, "hip", low, extra), _HIP_PRELUDE.strip(), "",
-                      _hip_kernel_text(kernel, config, plan, low, args, geo), ""])
+                      _hip_kernel_text(kernel, config, plan, low, args, geo, scratch_arg), ""])
 
 
 def emit_hip_host(kernel: Kernel, config: Config) -> str:

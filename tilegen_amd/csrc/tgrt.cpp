@@ -115,6 +115,8 @@ void tg_clear_error(void) {
   g_message[0] = '\0';
 }
 
+int tg_fail(int code, const char* message) { return fail(code, "%s", message ? message : ""); }
+
 int tg_device_count(int* count) {
   if (!count) return fail(-1, "tg_device_count: null output");
   *count = 0;

@@ -61,6 +61,7 @@ def _declare(L) -> None:
         "tg_last_error": (ctypes.c_char_p, []),
         "tg_last_status": (ctypes.c_int, []),
         "tg_clear_error": (None, []),
+        "tg_fail": (ctypes.c_int, [ctypes.c_int, ctypes.c_char_p]),
         "tg_device_count": (ctypes.c_int, [_c_int_p]),
         "tg_set_device": (ctypes.c_int, [ctypes.c_int]),
         "tg_get_device": (ctypes.c_int, [_c_int_p]),
@@ -126,6 +127,29 @@ def lib():
             _declare(L)
             _LIB = L
     return _LIB
+
+
+_NOALLOC = None
+
+
+def noalloc_lib():
+    """libtgna.so (include/tilegen_noalloc.h), loaded after libtgrt.  Raises
+    TileGenHipError when it was never built."""
+    global _NOALLOC
+    if _NOALLOC is not None:
+        return _NOALLOC
+    lib()
+    with _LOCK:
+        if _NOALLOC is None:
+            path = os.path.join(lib_dir(), "libtgna.so")
+            if not os.path.exists(path):
+                raise TileGenHipError("libtgna.so is not built (%s); run "
+                                      "__graft_entry__.build()" % path)
+            L = ctypes.CDLL(path)
+            L.launch_spmv_noalloc.argtypes = [_vp] * 5 + [ctypes.c_int64] * 3 + [_vp]
+            L.launch_spmv_noalloc.restype = ctypes.c_int
+            _NOALLOC = L
+    return _NOALLOC
 
 
 def last_error() -> str:
