@@ -133,3 +133,17 @@ def test_no_packed_fp32_in_generated_code(tmp_path):
         assert "v_pk_fma_f32" not in asm and "v_pk_add_f32" not in asm and \
             "v_pk_mul_f32" not in asm
         assert "scratch_" not in asm  # no register spills
+
+
+def test_noalloc_library_exports_its_header():
+    """libtgna.so exports exactly what include/tilegen_noalloc.h declares and
+    loads without a GPU."""
+    import os as _os
+    path = _os.path.join(runtime.lib_dir(), "libtgna.so")
+    declared = _declared("tilegen_noalloc.h")
+    assert declared == ["launch_spmv_noalloc"]
+    exported = _exported(path)
+    assert sorted(exported & set(declared)) == declared
+    assert not [s for s in exported if s.startswith(("tg_", "tgv_", "spmv_"))]
+    L = runtime.noalloc_lib()
+    assert L.launch_spmv_noalloc.restype is ctypes.c_int
