@@ -1,7 +1,8 @@
 """(CPU) The merge-path partition of the nnz-balanced SpMV kernels.
 
 ``mp_search`` restates the device search ``tg_mp_search`` lane for lane (64
-probes per round, the same first-round pattern, clamping and bracket update);
+probes per round ascending with the lane, the same first-round pattern,
+clamping, and the bracket update from the ballot's first passing lane);
 ``partition`` restates the window set-up the emitter writes for every
 workgroup (window bounds, first/last row, the pieces of rows longer than a
 window, the rows summed whole).  The tests check them against what the
@@ -33,24 +34,37 @@ from tilegen_amd.codegen import Config
 from tilegen_amd.matrices import make_baseline
 
 
+def first_probes(g: int):
+    """The first round's probe of each lane around the guess g (``tg_mp_probe``):
+    8 rows at growing distances below, 48 consecutive, 8 at growing distances
+    above, ascending with the lane."""
+    return [g - 24 - (32 << (2 * (7 - l))) if l < 8 else
+            (g - 32 + l if l < 56 else g + 24 + (32 << (2 * (l - 56)))) for l in range(64)]
+
+
+def _ends(qs, passed):
+    """The lanes the ballot names: the first that passes (None: none) and the
+    one before it (None: the first lane passes).  The probes ascend with the
+    lane and the test is monotone in the row, so the passing lanes are exactly
+    the lanes from the first on."""
+    assert all(qs[i] <= qs[i + 1] for i in range(63)), "probes must ascend with the lane"
+    f = next((i for i, p in enumerate(passed) if p), None)
+    assert f is None or all(passed[f:]), "the test must be monotone in the probed row"
+    return f, (63 if f is None else (f - 1 if f > 0 else None))
+
+
 def mp_search(indptr, R: int, t: int, X: int):
     """Lane-for-lane model of ``tg_mp_search``: (answer, rounds, probed rows)."""
     g = int(float(t) * (float(R) / float(X))) if X > 0 else 0
-    qs = []
-    for l in range(64):
-        if l < 48:
-            qs.append(g - 24 + l)
-        else:
-            d = 32 << (2 * ((l - 48) >> 1))
-            qs.append(g + 24 + d if l & 1 else g - 24 - d)
+    qs = first_probes(g)
     lo, hi, rounds, probed = 0, R, 0, set()
     while True:
         rounds += 1
         qs = [min(max(q, lo), hi) for q in qs]
         probed.update(qs)
-        ge = [q + int(indptr[q]) >= t for q in qs]
-        a = max([lo - 1] + [q for q, g_ in zip(qs, ge) if not g_])
-        b = min([hi] + [q for q, g_ in zip(qs, ge) if g_])
+        f, fa = _ends(qs, [q + int(indptr[q]) >= t for q in qs])
+        b = qs[f] if f is not None else hi
+        a = qs[fa] if fa is not None else lo - 1
         lo, hi = a + 1, b
         if lo >= hi:
             return hi, rounds, probed
@@ -205,7 +219,7 @@ def test_merge_source_and_refusals():
     cfg = Config(tile_size=64, threads_per_row=8, unroll=2, block_size=512, balance="nnz")
     for k in ("spmv", "fused_spmv_axpy"):
         g = cg.generate(ks[k], cfg, backend="hip", write=False)
-        assert "tg_mp_search(indptr, row_lim, t0, X, 1)" in g.source
+        assert "tg_mp_search(indptr, row_lim, t0, X)" in g.source
         assert "tg_mp_commit(tg_part, wdx, wf, wl, t, &tot)" in g.source
         tiling = [e for e in cg._passes.run_pipeline(ks[k], cfg, backend="hip").pass_log
                   if e["pass"] == "tiling"][0]
@@ -228,27 +242,55 @@ def test_merge_source_and_refusals():
 # --------------------------------------------------------------------------- #
 # hybrid tiles: row tiles plus long-row workgroups over equal nonzero ranges
 # --------------------------------------------------------------------------- #
+def _row_at(indptr, R, P, X):
+    """``tg_mp_row`` lane for lane: the row holding nonzero P with its bounds,
+    and the number of probe rounds it took."""
+    qs = first_probes(int(float(P) * (float(R) / float(X))))
+    lo, hi, vlo, vhi = 0, R, 0, X
+    rounds = 0
+    while True:
+        rounds += 1
+        qs = [min(max(q, lo), hi) for q in qs]
+        vs = [int(indptr[q]) for q in qs]
+        f, fa = _ends(qs, [v > P for v in vs])
+        if f is not None:
+            hi, vhi = qs[f], vs[f]
+        if fa is not None:
+            lo, vlo = qs[fa], vs[fa]
+        if hi - lo <= 1:
+            return lo, vlo, vhi, rounds
+        s = (hi - lo + 61) // 63
+        qs = [lo + 1 + l * s for l in range(64)]
+
+
+def hybrid_listed(indptr, M: int, CH: int, e: int):
+    """The long rows range e lists, as (row, start, end): the distinct rows
+    longer than CH / 2 among those holding nonzeros p0, p0 + CH / 2 (p1 - 1 when
+    that lies past the range) and p1 - 1."""
+    nnz = int(indptr[M])
+    LH = CH // 2
+    p0, p1 = e * CH, min(e * CH + CH, nnz)
+    found = [_row_at(indptr, M, P, nnz)[:3]
+             for P in (p0, p0 + LH if p0 + LH < p1 else p1 - 1, p1 - 1)]
+    out = []
+    for k, (r, rs, re) in enumerate(found):
+        if re - rs > LH and (k == 0 or r != found[k - 1][0]):
+            out.append((r, rs, re))
+    return out
+
+
 def hybrid_pieces(indptr, M: int, CH: int, cap: int = cg.MERGE_CAP):
     """The long-row workgroups as the emitter writes them: for every range e,
     the (row, begin, end, ef, el, e, cut) pieces it sums, and the number of
     rows it listed."""
     nnz = int(indptr[M])
-    LH = CH // 2
     GL = -(-nnz // CH) if nnz > 0 else 0
     out, listed = [], []
     for e in range(GL):
         p0, p1 = e * CH, min(e * CH + CH, nnz)
-        ra = max(0, _search0(indptr, M, p0 + 1, nnz) - 1)  # the row holding nonzero p0
-        rows = []
-        r = ra
-        while r < M and int(indptr[r]) < p1:
-            rs, re = int(indptr[r]), int(indptr[r + 1])
-            if re - rs > LH and re > p0:
-                rows.append(r)
-            r += 1
+        rows = hybrid_listed(indptr, M, CH, e)
         listed.append(len(rows))
-        for row in rows:
-            rs, re = int(indptr[row]), int(indptr[row + 1])
+        for row, rs, re in rows:
             ef, el = rs // CH, (re - 1) // CH
             cut = el > ef and el < cap
             if not cut and ef != e:
@@ -259,23 +301,49 @@ def hybrid_pieces(indptr, M: int, CH: int, cap: int = cg.MERGE_CAP):
     return out, listed
 
 
-def _search0(indptr, R, t, nnz):
-    """``tg_mp_search`` with row weight 0 (nonzero positions)."""
-    g = int(float(t) * (float(R) / float(nnz))) if nnz > 0 else 0
-    qs = [g - 24 + l if l < 48 else
-          (g + 24 + (32 << (2 * ((l - 48) >> 1))) if l & 1 else
-           g - 24 - (32 << (2 * ((l - 48) >> 1)))) for l in range(64)]
-    lo, hi = 0, R
-    while True:
-        qs = [min(max(q, lo), hi) for q in qs]
-        ge = [int(indptr[q]) >= t for q in qs]
-        a = max([lo - 1] + [q for q, g_ in zip(qs, ge) if not g_])
-        b = min([hi] + [q for q, g_ in zip(qs, ge) if g_])
-        lo, hi = a + 1, b
-        if lo >= hi:
-            return hi
-        s = (hi - lo + 62) // 63
-        qs = [lo + l * s for l in range(64)]
+def test_row_search_finds_the_row_holding_a_nonzero():
+    """The row search returns the row holding nonzero P (numpy searchsorted on
+    the row pointers) and that row's two bounds, within a few rounds."""
+    for label, A in _cases():
+        ip = np.asarray(A.indptr, dtype=np.int64)
+        M, nnz = A.shape[0], int(ip[-1])
+        if nnz == 0:
+            continue
+        for t in sorted(set([0, nnz - 1, nnz // 2] + list(np.random.default_rng(1).integers(
+                0, nnz, size=100)))):
+            r, rs, re, rounds = _row_at(ip, M, int(t), nnz)
+            assert r == int(np.searchsorted(ip, t, side="right")) - 1, (label, t)
+            assert (rs, re) == (int(ip[r]), int(ip[r + 1])) and rs <= t < re
+            assert rounds <= 2 + int(np.ceil(np.log(max(M, 2)) / np.log(63))), (label, t, rounds)
+
+
+def test_row_search_with_empty_rows_everywhere():
+    """Runs of empty rows before, between and after the nonzeros: the row found
+    is the nonempty one holding P."""
+    lens = np.zeros(5000, dtype=np.int64)
+    lens[[7, 8, 1999, 2000, 4990]] = [3, 1, 40, 2, 9]
+    ip = np.concatenate([[0], np.cumsum(lens)])
+    nnz = int(ip[-1])
+    for t in range(nnz):
+        r, rs, re, _ = _row_at(ip, len(lens), t, nnz)
+        assert lens[r] > 0 and rs <= t < re and (rs, re) == (ip[r], ip[r + 1])
+
+
+@pytest.mark.parametrize("CH", [128, 512, 2048])
+def test_ranges_list_every_long_row_meeting_them(CH):
+    """The rows a range lists are exactly the rows longer than CH / 2 that meet
+    [p0, p1), with their bounds, and never more than 3 of them."""
+    LH = CH // 2
+    for label, A in _cases():
+        ip = np.asarray(A.indptr, dtype=np.int64)
+        M, nnz = A.shape[0], int(ip[-1])
+        lens = np.diff(ip)
+        for e in range(-(-nnz // CH) if nnz else 0):
+            p0, p1 = e * CH, min(e * CH + CH, nnz)
+            want = [int(r) for r in np.nonzero((lens > LH) & (ip[1:] > p0) & (ip[:-1] < p1))[0]]
+            got = hybrid_listed(ip, M, CH, e)
+            assert [r for r, _, _ in got] == want and len(got) <= 3, (label, CH, e)
+            assert all((rs, re) == (int(ip[r]), int(ip[r + 1])) for r, rs, re in got)
 
 
 @pytest.mark.parametrize("CH", [128, 512, 2048, 4096])
@@ -317,7 +385,7 @@ def test_hybrid_source_and_geometry():
     ks = dsl.standard_kernels()
     cfg = Config(tile_size=64, threads_per_row=8, unroll=2, block_size=512, balance="hybrid")
     g = cg.generate(ks["spmv"], cfg, backend="hip", write=False)
-    assert "tg_mp_search(indptr, row_end, p0 + 1, nnz, 0)" in g.source
+    assert "tg_mp_row(indptr, row_end, P, nnz, &rs, &re)" in g.source
     assert "(nnz + 2048 - 1) / 2048" in g.host_source
     assert g.geometry.grid(100000, 794591) == 1563 + 388
     assert g.geometry.grid(0, 5) == 0 and g.geometry.grid(10, 0) == 1

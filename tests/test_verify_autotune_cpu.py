@@ -72,7 +72,8 @@ def test_hip_compile_only_without_device(tmp_path):
 
 def test_hip_compile_error_is_reported(tmp_path):
     gen = generate(standard_kernels()["spmv"], Config(), "hip", outdir=str(tmp_path))
-    gen.source = gen.source.replace("acc[r] += ", "acc[r] += undefined_symbol + ")
+    gen.source = gen.source.replace("acc[r] = ok[u] ? acc[r] + ", "acc[r] = ok[u] ? undefined_symbol + ")
+    assert "undefined_symbol" in gen.source
     with pytest.raises(RuntimeError) as err:
         compile_generated(gen, "hip", str(tmp_path))
     assert "undefined_symbol" in str(err.value)

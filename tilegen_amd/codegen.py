@@ -786,40 +786,72 @@ def _merge_decls(pre: _W, scratch_arg: bool = False) -> None:
 // nonzeros, then one item that ends it); the launch's items are cut into one
 // window per workgroup.
 //
-// Smallest r in [0, R] with wt * r + indptr[r] >= t (R when there is none), for
-// wt 1 (merge-path items) or 0 (nonzero positions); X = wt * R + nnz.  Run by
-// all 64 lanes of one wave, one row pointer per lane per round.  The first round
-// probes 48 consecutive rows around the proportional guess and 16 rows at
-// growing distances either side of it; each later round probes 64 evenly spaced
-// rows of the bracket left, so the bracket shrinks at least 63-fold per round.
-__device__ tg_i64 tg_mp_search(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 t, tg_i64 X,
-                               int wt) {
+// Value of v held by lane src (uniform) of the wave.
+__device__ __forceinline__ tg_i64 tg_lane_read(tg_i64 v, int src) {
+  const int lo = __builtin_amdgcn_readlane((int)v, src);
+  const int hi = __builtin_amdgcn_readlane((int)(v >> 32), src);
+  return ((tg_i64)hi << 32) | (tg_i64)(unsigned)lo;
+}
+
+// First-round probe of lane l around the guess g, ascending with l: 8 rows at
+// growing distances below g, 48 consecutive rows around it, 8 at growing
+// distances above.  Every round's probes ascend with the lane, so the lanes
+// whose row passes a monotone test are the ones from the first such lane on.
+__device__ __forceinline__ tg_i64 tg_mp_probe(tg_i64 g, int l) {
+  if (l < 8) return g - 24 - ((tg_i64)32 << (2 * (7 - l)));
+  if (l < 56) return g - 32 + l;
+  return g + 24 + ((tg_i64)32 << (2 * (l - 56)));
+}
+
+// Smallest r in [0, R] with r + indptr[r] >= t (R when there is none);
+// X = R + nnz.  Run by all 64 lanes of one wave, one row pointer per lane per
+// round; the ballot of the test gives the bracket's new ends (the first lane
+// that passes and the lane before it), read from those lanes.  Each later round
+// probes 64 evenly spaced rows of the bracket left, so the bracket shrinks at
+// least 63-fold per round.
+__device__ tg_i64 tg_mp_search(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 t, tg_i64 X) {
   const int l = threadIdx.x & 63;
   const tg_i64 g = X > 0 ? (tg_i64)((double)t * ((double)R / (double)X)) : 0;
-  tg_i64 q;
-  if (l < 48) {
-    q = g - 24 + l;
-  } else {
-    const tg_i64 d = (tg_i64)32 << (2 * ((l - 48) >> 1));
-    q = (l & 1) ? g + 24 + d : g - 24 - d;
-  }
+  tg_i64 q = tg_mp_probe(g, l);
   tg_i64 lo = 0, hi = R;
   #pragma unroll 1
   for (;;) {
     q = q < lo ? lo : (q > hi ? hi : q);
-    const bool ge = (wt ? q : 0) + indptr[q] >= t;
-    tg_i64 a = ge ? lo - 1 : q;   // rows known to start before t
-    tg_i64 b = ge ? q : hi;       // rows known to start at or after t
-    #pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-      const tg_i64 a2 = tg_lane_bcast(a, l ^ m), b2 = tg_lane_bcast(b, l ^ m);
-      a = a2 > a ? a2 : a;
-      b = b2 < b ? b2 : b;
-    }
+    const unsigned long long m = __ballot(q + indptr[q] >= t);
+    const int f = m ? (int)__builtin_ctzll(m) : 64;   // first lane that passes
+    const tg_i64 b = f < 64 ? tg_lane_read(q, f) : hi;
+    const tg_i64 a = f > 0 ? tg_lane_read(q, f - 1) : lo - 1;   // rows before t
     lo = a + 1;
     hi = b;
     if (lo >= hi) return hi;
     q = lo + (tg_i64)l * ((hi - lo + 62) / 63);
+  }
+}
+
+// The row holding nonzero position P, 0 <= P < X = indptr[R]: the one row r with
+// indptr[r] <= P < indptr[r + 1], returned with those two bounds in *rs and
+// *re.  Run by all 64 lanes of one wave, with the probes of tg_mp_search; the
+// bracket [lo, hi] keeps indptr[lo] <= P < indptr[hi] and carries both values,
+// so the bounds cost no load of their own.
+__device__ tg_i64 tg_mp_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 P, tg_i64 X,
+                            tg_i64* rs, tg_i64* re) {
+  const int l = threadIdx.x & 63;
+  tg_i64 q = tg_mp_probe((tg_i64)((double)P * ((double)R / (double)X)), l);
+  tg_i64 lo = 0, hi = R, vlo = 0, vhi = X;   // indptr[0] = 0, indptr[R] = X
+  #pragma unroll 1
+  for (;;) {
+    q = q < lo ? lo : (q > hi ? hi : q);
+    const tg_i64 v = indptr[q];
+    const unsigned long long m = __ballot(v > P);
+    const int f = m ? (int)__builtin_ctzll(m) : 64;   // first lane past P
+    if (f < 64) { hi = tg_lane_read(q, f); vhi = tg_lane_read(v, f); }
+    if (f > 0) { lo = tg_lane_read(q, f - 1); vlo = tg_lane_read(v, f - 1); }
+    if (hi - lo <= 1) {
+      *rs = vlo;
+      *re = vhi;
+      return lo;
+    }
+    q = lo + 1 + (tg_i64)l * ((hi - lo + 61) / 63);   // rows strictly inside the bracket
   }
 }
 
@@ -901,14 +933,14 @@ def _merge_window(w: _W, TR: int, WAVES: int) -> None:
     w("const tg_i64 t1 = t0 + D < X ? t0 + D : X;")
     w("// first and last rows: the first row beginning at or after t0 (t1)")
     w.open("if (threadIdx.x < 64)")
-    w("const tg_i64 a = wdx == 0 ? 0 : tg_mp_search(indptr, row_lim, t0, X, 1);")
+    w("const tg_i64 a = wdx == 0 ? 0 : tg_mp_search(indptr, row_lim, t0, X);")
     w("if (threadIdx.x == 0) s_win[0] = a;")
     w("if (threadIdx.x < 2) s_win[2 + threadIdx.x] = a - 1 + (tg_i64)threadIdx.x >= 0 ? "
       "indptr[a - 1 + threadIdx.x] : 0;")
     w.close()
     sel = "threadIdx.x >= 64 && threadIdx.x < 128" if WAVES > 1 else "threadIdx.x < 64"
     w.open("if (%s)" % sel)
-    w("const tg_i64 b = wdx == G - 1 ? row_lim : tg_mp_search(indptr, row_lim, t1, X, 1);")
+    w("const tg_i64 b = wdx == G - 1 ? row_lim : tg_mp_search(indptr, row_lim, t1, X);")
     w("const int l = threadIdx.x & 63;")
     w("if (l == 0) s_win[1] = b;")
     w("if (l < 2) s_win[4 + l] = b - 1 + l >= 0 ? indptr[b - 1 + l] : 0;")
@@ -925,92 +957,191 @@ def _merge_window(w: _W, TR: int, WAVES: int) -> None:
     w("const tg_i64 r_own = pc_out ? r1 - 1 : r1;  // rows summed whole, %d at a time" % TR)
 
 
+def _value_row_free(plan: Plan) -> bool:
+    """Whether the per-nonzero value reads only the sparse value and the
+    gathered operand (so it can be formed before the row is known)."""
+    g = _gather_operand(plan)
+    for n in plan.value_expr.walk():
+        if isinstance(n, Access) and n is not g and not n.tensor.format.is_sparse() \
+                and n.tensor.order > 0:
+            return False
+    return True
+
+
 def _hybrid_ranges(w: _W, plan: Plan, step, out_name: str, B: int, U: int, ALIGN: int,
                    WAVES: int, CH: int, LH: int) -> None:
     """The long-row workgroups of hybrid tiles (defines GL; those workgroups
-    return).  Workgroup e < GL takes nonzeros [e CH, (e+1) CH): it finds the
-    row holding the first of them with ``tg_mp_search``, lists the rows from
-    there on that are longer than LH and meet the range, and sums each one's
-    part in the range with the whole workgroup.  A row within one range is
-    written directly; a row spanning ranges is combined by ``tg_mp_commit``
-    (its pieces in range order), or, when its last range has no scratch slot,
-    summed whole by its first range."""
+    return).  Workgroup e < GL takes nonzeros [p0, p1) = [e CH, (e+1) CH).
+
+    A row longer than LH = CH / 2 that meets the range holds p0, p0 + LH or
+    p1 - 1, so three waves (one each) find the rows holding those positions
+    with ``tg_mp_row``, which returns each row's bounds with it: no scan of
+    the rows in between.  The distinct ones longer than LH are the listed
+    rows.  All of their nonzeros in the range are then loaded and gathered
+    together, each lane holding a fixed set of positions (every load and
+    gather issued before any is used), and each lane adds its products into
+    the listed rows in a fixed order.  The workgroup reduces each row's
+    partial; wave k writes row k directly when the row lies within one range,
+    or combines it with the row's other pieces by ``tg_mp_commit`` (in range
+    order).  A row whose last range has no scratch slot is summed whole by its
+    first range.  The row tiles own every other row."""
     row = plan.row_idx.name
+    NS = CH // (B * U)
+    if NS * B * U != CH:
+        raise ValueError("hybrid range of %d nonzeros is not a whole number of workgroup "
+                         "steps (%d)" % (CH, B * U))
+    if not _value_row_free(plan):
+        raise ValueError("hybrid tiles need a per-nonzero value that reads only the sparse "
+                         "value and the gathered operand")
+    gathered = _gather_operand(plan)
+    col = plan.col_idx.name
     w("// workgroups below GL sum the rows longer than %d nonzeros, %d nonzeros each;" % (LH, CH))
     w("// the rest are row tiles, which leave those rows alone")
     w("const tg_i64 GL = nnz > 0 ? (nnz + %d) / %d : 0;" % (CH - 1, CH))
     w.open("if ((tg_i64)blockIdx.x < GL)")
-    w("__shared__ tg_i64 s_ra;")
-    w("__shared__ tg_i64 s_lr[8];  // long rows meeting the range (at most 3)")
-    w("__shared__ int s_nl;")
-    w("__shared__ double s_hred[%d];" % WAVES)
+    w("__shared__ tg_i64 s_lr[9];  // the rows holding p0, p0 + LH, p1 - 1: row, start, end")
+    w("__shared__ double s_hred[%d];  // [wave][listed row]" % (3 * WAVES))
+    w("__shared__ double s_kred[%d];" % WAVES)
     w("const tg_i64 e = blockIdx.x;")
     w("const tg_i64 p0 = e * %d, p1 = p0 + %d < nnz ? p0 + %d : nnz;" % (CH, CH, CH))
-    w("// the row holding nonzero p0: one before the first row that begins past it")
-    w.open("if (threadIdx.x < 64)")
-    w("const tg_i64 a = tg_mp_search(indptr, row_end, p0 + 1, nnz, 0) - 1;")
-    w("if (threadIdx.x == 0) { s_ra = a < 0 ? 0 : a; s_nl = 0; }")
+    w("const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);")
+    def load_range(sel: Callable[[int, str], str]) -> None:
+        """Indices and values of lane l's positions p0 + s B U + l U + u in hi_/hv_,
+        with every load issued unconditionally (a load under a lane-varying branch
+        is waited for before the branch joins).  ``sel(s, q)`` is the lane's
+        condition to load its own positions; other lanes load the range's first
+        ones, which the wave shares.  Positions are masked when used."""
+        w("tg_i64 hi_[%d]; double hv_[%d];" % (NS * U, NS * U))
+        for s_ in range(NS):
+            q = "qs%d" % s_
+            w("const tg_i64 %s = p0 + %d + (tg_i64)threadIdx.x * %d;" % (q, s_ * B * U, U))
+            w("const tg_i64 qe%d = %s ? %s : p0;" % (s_, sel(s_, q), q))
+        if U % 2 == 0:
+            w("// whole range, 16-byte aligned bases: 128-bit pairs for every lane")
+            w.open("if (pair_ok && p1 - p0 == %d)" % CH)
+            for s_ in range(NS):
+                for u in range(0, U, 2):
+                    o = s_ * U + u
+                    w("{ const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + qe%d + %d));"
+                      " hi_[%d] = a.x; hi_[%d] = a.y; }" % (s_, u, o, o + 1))
+                    w("{ const tg_f64x2 b = __builtin_nontemporal_load((const tg_f64x2*)(data + qe%d + %d));"
+                      " hv_[%d] = b.x; hv_[%d] = b.y; }" % (s_, u, o, o + 1))
+            w.close()
+            w.open("else")
+        else:
+            w.open("")
+        w("// the last range, or bases only 8-byte aligned: per element, clamped into the arrays")
+        for s_ in range(NS):
+            for u in range(U):
+                o = s_ * U + u
+                w("{ const tg_i64 c = qe%d + %d < nnz ? qe%d + %d : nnz - 1;"
+                  " hi_[%d] = __builtin_nontemporal_load(indices + c);"
+                  " hv_[%d] = __builtin_nontemporal_load(data + c); }" % (s_, u, s_, u, o, o))
+        w.close()
+
+    w("// a row longer than %d that meets [p0, p1) holds p0, p0 + %d or p1 - 1 (one lying" % (LH, LH))
+    w("// strictly inside the range is longer than half of it, so it holds the middle):")
+    w("// wave k finds the row holding the k-th of those positions, with its bounds")
+    w("#pragma unroll 1")
+    w.open("for (int k = wv; k < 3; k += %d)" % WAVES)
+    w("const tg_i64 P = k == 0 ? p0 : (k == 1 && p0 + %d < p1 ? p0 + %d : p1 - 1);" % (LH, LH))
+    w("tg_i64 rs, re;")
+    w("const tg_i64 r = tg_mp_row(indptr, row_end, P, nnz, &rs, &re);")
+    w("if ((threadIdx.x & 63) == 0) { s_lr[3 * k] = r; s_lr[3 * k + 1] = rs; s_lr[3 * k + 2] = re; }")
     w.close()
     w("__syncthreads();")
-    w("const tg_i64 ra = s_ra;")
-    w("// rows from ra on, up to the first that begins at or past p1")
+    w("// the distinct long rows among them (the positions ascend, so a row found twice is")
+    w("// found by neighbouring waves)")
+    w("tg_i64 kr[3], ks[3], ke[3];")
+    w("bool kl[3];")
+    w("#pragma unroll")
+    w.open("for (int k = 0; k < 3; ++k)")
+    w("kr[k] = tg_uniform(s_lr[3 * k]); ks[k] = tg_uniform(s_lr[3 * k + 1]); "
+      "ke[k] = tg_uniform(s_lr[3 * k + 2]);")
+    w("kl[k] = ke[k] - ks[k] > %d && (k == 0 || kr[k] != s_lr[3 * k - 3]);" % LH)
+    w.close()
+    w("if (!kl[0] && !kl[1] && !kl[2]) return;  // no long row meets this range")
+    w("// the listed rows' nonzeros in this range: lane l holds p0 + s * %d + l * %d + u" % (
+        B * U, U))
+    load_range(lambda s_, q: "((%s < p1) & ((kl[0] & (%s + %d > ks[0]) & (%s < ke[0])) | "
+               "(kl[1] & (%s + %d > ks[1]) & (%s < ke[1])) | (kl[2] & (%s + %d > ks[2]) & "
+               "(%s < ke[2]))))" % (q, q, U, q, q, U, q, q, U, q))
+    w("// the products of the listed rows' nonzeros in this range: every gather is issued")
+    w("// (other positions gather element 0) before any is used, then the products are")
+    w("// selected, so a non-finite x[0] cannot leak in")
+    w("double xg_[%d]; bool mk_[%d];" % (NS * U, NS * U))
+    for s_ in range(NS):
+        w("#pragma unroll")
+        w.open("for (int u = 0; u < %d; ++u)" % U)
+        w("const tg_i64 pu = qs%d + u;" % s_)
+        w("mk_[%d + u] = (pu < p1) & ((kl[0] & (pu >= ks[0]) & (pu < ke[0])) | "
+          "(kl[1] & (pu >= ks[1]) & (pu < ke[1])) | (kl[2] & (pu >= ks[2]) & (pu < ke[2])));"
+          % (s_ * U))
+        w("const tg_i64 cu = mk_[%d + u] ? hi_[%d + u] : 0;" % (s_ * U, s_ * U))
+        w("xg_[%d + u] = %s;" % (s_ * U, _cexpr(gathered, _Env({row: "0", col: "cu"}, p="pu"))))
+        w.close()
+    w("// each lane's products, into the listed rows they belong to, in a fixed order")
+    w("double part[3] = {0.0, 0.0, 0.0};")
+    w("#pragma unroll")
+    w.open("for (int i = 0; i < %d; ++i)" % (NS * U))
+    w("const tg_i64 pu = p0 + (i / %d) * %d + (tg_i64)threadIdx.x * %d + i %% %d;"
+      % (U, B * U, U, U))
+    w("const double pv = mk_[i] ? %s : 0.0;" % _value_with(plan, "hv_[i]", "xg_[i]", "0", "hi_[i]"))
+    w("#pragma unroll")
+    w("for (int k = 0; k < 3; ++k) part[k] += (kl[k] & (pu >= ks[k]) & (pu < ke[k])) ? pv : 0.0;")
+    w.close()
+    w("// then the workgroup's, per listed row")
+    w("#pragma unroll")
+    w.open("for (int k = 0; k < 3; ++k)")
+    w.open("if (kl[k])")
+    w("const double t = tg_segsum<64>(part[k]);")
+    w("if ((threadIdx.x & 63) == 0) s_hred[3 * wv + k] = t;")
+    w.close()
+    w.close()
+    w("__syncthreads();")
+    w("// wave k writes or combines listed row k")
     w("#pragma unroll 1")
-    w.open("for (tg_i64 base = ra; ; base += %d)" % B)
-    w("const tg_i64 r = base + (tg_i64)threadIdx.x;")
-    w("bool past = true;")
-    w.open("if (r < row_end)")
-    w("const tg_i64 rs = indptr[r];")
-    w("past = rs >= p1;")
-    w.open("if (!past)")
-    w("const tg_i64 re = indptr[r + 1];")
-    w.open("if (re - rs > %d && re > p0)" % LH)
-    w("const int k = atomicAdd(&s_nl, 1);")
-    w("if (k < 8) s_lr[k] = r;")
-    w.close()
-    w.close()
-    w.close()
-    w("if (__syncthreads_or(past)) break;")
-    w.close()
-    w("const int nl = s_nl < 8 ? s_nl : 8;")
-    w("#pragma unroll 1")
-    w.open("for (int k = 0; k < nl; ++k)")
-    w("const tg_i64 row = s_lr[k];")
-    w("const tg_i64 rs = indptr[row], re = indptr[row + 1];")
+    w.open("for (int k = wv; k < 3; k += %d)" % WAVES)
+    w("const tg_i64 r = s_lr[3 * k], rs = s_lr[3 * k + 1], re = s_lr[3 * k + 2];")
+    w("if (!(re - rs > %d && (k == 0 || r != s_lr[3 * k - 3]))) continue;" % LH)
     w("const tg_i64 ef = rs / %d, el = (re - 1) / %d;  // the ranges its nonzeros lie in"
       % (CH, CH))
     w("const bool cut = el > ef && el < %d;" % MERGE_CAP)
-    w("if (!cut && ef != e) continue;  // kept whole: summed by its first range only")
-    w("const tg_i64 q0 = cut && p0 > rs ? p0 : rs, q1 = cut && p1 < re ? p1 : re;")
-    w("double cacc = 0.0, cacc2 = 0.0;")
-    w("// a piece spans at most two workgroup steps (plus one element of alignment):")
-    w("// both steps' loads go out together, the rest (whole rows) loops")
-    w("const tg_i64 qa = (q0 & ~(tg_i64)%d) + (tg_i64)threadIdx.x * %d, qb = qa + %d;"
-      % (ALIGN - 1, U, B * U))
-    w.open("if (qa < q1)")
-    step("qa", "q0", "q1", "cacc")
-    w.close()
-    w.open("if (qb < q1)")
-    step("qb", "q0", "q1", "cacc2")
-    w.close()
-    w("cacc += cacc2;")
-    w("#pragma unroll 1")
-    w.open("for (tg_i64 q = qb + %d; q < q1; q += %d)" % (B * U, B * U))
-    step("q", "q0", "q1", "cacc")
-    w.close()
-    w("cacc = tg_segsum<64>(cacc);")
-    w("if ((threadIdx.x & 63) == 0) s_hred[threadIdx.x >> 6] = cacc;")
-    w("__syncthreads();")
-    w.open("if (threadIdx.x < 64)")
+    w("if (!cut && el != ef) continue;  // kept whole: summed by its first range below")
     w("double t = 0.0;")
     w("#pragma unroll")
-    w("for (int v = 0; v < %d; ++v) t += s_hred[v];" % WAVES)
+    w("for (int v = 0; v < %d; ++v) t += s_hred[3 * v + k];" % WAVES)
     w("double tot = t;")
     w("const bool done = !cut || tg_mp_commit(tg_part, e, ef, el, t, &tot);")
-    w.open("if (done && threadIdx.x == 0)")
+    w.open("if (done && (threadIdx.x & 63) == 0)")
+    w("const tg_i64 row = r;")
     env = _Env({row: "row"}, acc="tot")
     w("__builtin_nontemporal_store(%s, %s + %s);" % (
         _cexpr(plan.final_expr, env), out_name, _offset(plan.out_tensor, plan.out.indices, env)))
     w.close()
+    w.close()
+    w("// rows reaching past the scratch's last range are summed whole by their first range")
+    w("#pragma unroll 1")
+    w.open("for (int k = 0; k < 3; ++k)")
+    w("const tg_i64 row = s_lr[3 * k], rs = s_lr[3 * k + 1], re = s_lr[3 * k + 2];")
+    w("if (!(re - rs > %d && (k == 0 || row != s_lr[3 * k - 3]))) continue;" % LH)
+    w("if (rs / %d != e || (re - 1) / %d < %d) continue;" % (CH, CH, MERGE_CAP))
+    w("double cacc = 0.0;")
+    w("#pragma unroll 1")
+    w.open("for (tg_i64 q = (rs & ~(tg_i64)%d) + (tg_i64)threadIdx.x * %d; q < re; q += %d)"
+           % (ALIGN - 1, U, B * U))
+    step("q", "rs", "re", "cacc")
+    w.close()
+    w("cacc = tg_segsum<64>(cacc);")
+    w("if ((threadIdx.x & 63) == 0) s_kred[wv] = cacc;")
+    w("__syncthreads();")
+    w.open("if (threadIdx.x == 0)")
+    w("double t = 0.0;")
+    w("#pragma unroll")
+    w("for (int v = 0; v < %d; ++v) t += s_kred[v];" % WAVES)
+    env = _Env({row: "row"}, acc="t")
+    w("__builtin_nontemporal_store(%s, %s + %s);" % (
+        _cexpr(plan.final_expr, env), out_name, _offset(plan.out_tensor, plan.out.indices, env)))
     w.close()
     w("__syncthreads();")
     w.close()
@@ -1082,18 +1213,21 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
             w("cv[%d] = %s + %d < nnz ? __builtin_nontemporal_load(data + %s + %d) : 0.0;"
               % (u, q, u, q, u))
         w.close()
-        w("double xv[%d];" % U)
+        w("double xv[%d]; bool ok[%d];" % (U, U))
+        w("// positions outside the row gather element 0 (every gather of the step is issued")
+        w("// before any is used) and leave the sum as it was, so a non-finite x[0] cannot")
+        w("// leak in")
         w("#pragma unroll")
         w.open("for (int u = 0; u < %d; ++u)" % U)
         w("const tg_i64 pu = %s + u;" % q)
-        w("const bool in_row = pu >= %s && pu < %s;" % (lo, hi))
-        w("cv[u] = in_row ? cv[u] : 0.0;")
-        w("ci[u] = in_row ? ci[u] : 0;")
+        w("ok[u] = (pu >= %s) & (pu < %s);" % (lo, hi))
+        w("ci[u] = ok[u] ? ci[u] : 0;")
         w("xv[u] = %s;" % _cexpr(gathered, _Env({row: "row", col: "ci[u]"}, p="pu")))
         w.close()
         w("#pragma unroll")
         w.open("for (int u = 0; u < %d; ++u)" % U)
-        w("%s += %s;" % (acc, _value_with(plan, "cv[u]", "xv[u]", row, "ci[u]")))
+        w("%s = ok[u] ? %s + %s : %s;" % (acc, acc, _value_with(plan, "cv[u]", "xv[u]", row,
+                                                                   "ci[u]"), acc))
         w.close()
 
     merge = coop and low.balance == "nnz"
