@@ -871,17 +871,42 @@ __device__ __forceinline__ void tg_mp_wait(unsigned long long v) {
 }
 
 // Wave: record window w's piece t of the row whose pieces lie in windows
-// wf..wl.  Lane 0 swaps the partial into its slot; once that swap has
+// wf..wl.
+//
+// Two pieces (wl = wf + 1): lane 0 swaps the partial into the first piece's
+// slot.  The piece whose swap is performed first finds the slot empty and
+// returns false; the other finds its partner's partial, sums the two in window
+// order, empties the slot and returns true with the sum in *tot.  One atomic
+// round trip.
+//
+// More pieces: lane 0 swaps the partial into its own slot; once that swap has
 // returned, the lanes read every slot of the row (compare-and-swaps that never
 // match, so they change nothing).  The piece whose swap is performed last finds every slot
 // full (any other piece's read of its slot came later); it may not be the only
 // one.  A piece that finds them all sums them in window order with a fixed
 // reduction tree, empties them and returns true with the sum in *tot; pieces
-// that find an empty slot return false.  Every combiner computes the same bits,
-// every slot is empty again when the launch ends, and no wave waits for another.
+// that find an empty slot return false.
+//
+// Either way every combiner computes the same bits, every slot is empty again
+// when the launch ends, and no wave waits for another.
 __device__ bool tg_mp_commit(unsigned long long* __restrict__ part, tg_i64 w, tg_i64 wf,
                              tg_i64 wl, double t, double* tot) {
   const int l = threadIdx.x & 63;
+  if (wl == wf + 1) {
+    unsigned long long other = 0;
+    if (l == 0)
+      other = __hip_atomic_exchange(part + 2 * wf + 1,
+                                    (unsigned long long)__double_as_longlong(t) ^ TG_MP_KEY,
+                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    other = (unsigned long long)__shfl((long long)other, 0);
+    if (other == 0) return false;
+    const double o = __longlong_as_double((long long)(other ^ TG_MP_KEY));
+    *tot = w == wf ? t + o : o + t;
+    if (l == 0)
+      (void)__hip_atomic_exchange(part + 2 * wf + 1, 0ull, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+  }
   unsigned long long mine = 0;
   if (l == 0)
     mine = __hip_atomic_exchange(part + 2 * w + (w == wf ? 1 : 0),

@@ -20,15 +20,17 @@ TUNED: Dict[str, Config] = {
     "c1": Config(tile_size=16, threads_per_row=8, unroll=2, vector_width=1, block_size=128),
     # 7 nonzeros per row: 4 lanes x 2
     "c2": Config(tile_size=128, threads_per_row=4, unroll=2, vector_width=1, block_size=256),
-    # skewed rows.  c3a: hybrid tiles, rows over 1024 nonzeros (half of a
-    # 2 x 256 x 4 range) summed by long-row workgroups over equal nonzero ranges,
-    # the rest on 4-lane groups (13.7 us against 17.4 with row tiles alone).
-    # c3b: hybrid tiles, rows over 512 nonzeros on ranges of 1024, the rest in
-    # tiles of 128 rows on 2-lane groups (10.3 us against 10.6 for the best row
-    # tiles, T32/TPR32/U2/B1024, in three interleaved repeats on one box)
+    # skewed rows, hybrid tiles: rows longer than half of a 2 x B x U nonzero range
+    # summed by long-row workgroups over equal ranges, the rest in row tiles.
+    # c3a: ranges of 2048 (rows over 1024), the rest on 4-lane groups in tiles of
+    # 64 rows (13.5 us against 17.4 with row tiles alone).  c3b: ranges of 2048,
+    # so each 2000-nonzero row has one or two pieces and combines in one atomic
+    # round trip, the rest in tiles of 128 rows on 4-lane groups (6.8 us, against
+    # 7.4 for ranges of 1024 and 10.6 for the best row tiles, T32/TPR32/U2/B1024;
+    # five interleaved repeats on one box)
     "c3a": Config(tile_size=64, threads_per_row=4, unroll=4, vector_width=1, block_size=256,
                   balance="hybrid"),
-    "c3b": Config(tile_size=128, threads_per_row=2, unroll=2, vector_width=1, block_size=256,
+    "c3b": Config(tile_size=128, threads_per_row=4, unroll=2, vector_width=1, block_size=512,
                   balance="hybrid"),
     # K = 64: 8 lanes x 2 columns x 4 passes per row, 2 nonzeros' B rows in flight
     # (fastest of all 882 legal SpMM schedules in a verified sweep on c4; 102.1 us
