@@ -73,7 +73,13 @@ def test_case_plan_counts_and_shared_grid(plans):
     assert [c for c, *_ in plan] == list(pf.CASE_ORDER)
     # headline: check + warmup + host-timed steps + warmup + event-timed steps
     assert by["c1"][2] == 1 + 2 * pf.WARMUP + 2 * pf.STEPS and by["c1"][3] == pf.STEPS
-    assert by["c2"][2] == 1 + pf.WARMUP + pf.CASE_ITERS
+    # the others: check + one launch per input copy + warmup + event-timed launches
+    from tilegen_amd.matrices import baseline_case, compulsory_bytes, make_baseline
+    A = make_baseline("c2")
+    copies = pf.bench_copies(compulsory_bytes("spmv", A.shape[0], A.shape[1], int(A.nnz), 1))
+    assert copies == 25  # 27.2 MB a launch: 640 MiB of rotation
+    assert by["c2"][2] == 1 + copies + pf.WARMUP + pf.CASE_ITERS
+    assert pf.bench_copies(1 << 40) == 2 and pf.bench_copies(1) == 64
     assert by["c5"][:2] == by["c5x25"][:2]  # same kernel and grid: told apart by order
     spmv = [g for c, (s, g, _n, _t) in by.items() if s == "spmv_kernel"]
     assert len(set(spmv)) == len(spmv)

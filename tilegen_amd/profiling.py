@@ -78,13 +78,25 @@ def valu_command(root: str = "rocprof_out") -> str:
             % (VALU_COUNTERS, root, BENCH_PMC))
 
 
+ROTATE_BYTES = 640 << 20
+
+
+def bench_copies(nbytes: int) -> int:
+    """Input copies bench.py rotates through (cold caches) for a case whose
+    launch moves ``nbytes`` compulsory bytes: about 640 MiB of them, 2 to 64."""
+    return int(min(64, max(2, -(-ROTATE_BYTES // max(int(nbytes), 1)))))
+
+
 def case_plan(steps: int, warmup: int, case_iters: int
               ) -> List[Tuple[str, str, int, int, int]]:
     """(case, kernel symbol, grid work-items, dispatches, event-timed dispatches)
-    of every case, in the order bench.py launches them."""
+    of every case, in the order bench.py launches them: one checked launch;
+    for the headline W warmup and K host-clocked steps, then W warmup and K
+    event-timed ones; for the others one launch per input copy, W warmup and
+    the event-timed ones."""
     from .codegen import _lowering, _plan
     from .dsl import standard_kernels
-    from .matrices import baseline_case, make_baseline
+    from .matrices import baseline_case, compulsory_bytes, make_baseline
     from .passes import run_pipeline
     from .schedules import TUNED
     from .codegen import launch_geometry
@@ -92,11 +104,17 @@ def case_plan(steps: int, warmup: int, case_iters: int
     for case in CASE_ORDER:
         bc = baseline_case(case)
         A = make_baseline(case)
+        M, N, nnz = A.shape[0], A.shape[1], int(A.nnz)
         k = run_pipeline(standard_kernels()[bc.kernel], TUNED[case], backend="hip")
         geo = launch_geometry(_plan(k), _lowering(k))
-        grid = geo.grid(A.shape[0], int(A.nnz)) * geo.block
-        timed = steps if case == HEADLINE else case_iters
-        n = 1 + warmup + timed + (warmup + steps if case == HEADLINE else 0)
+        grid = geo.grid(M, nnz) * geo.block
+        if case == HEADLINE:
+            timed = steps
+            n = 1 + warmup + steps + warmup + steps
+        else:
+            timed = case_iters
+            copies = bench_copies(compulsory_bytes(bc.kernel, M, N, nnz, bc.K))
+            n = 1 + copies + warmup + case_iters
         out.append((case, "%s_kernel" % bc.kernel, grid, n, timed))
     return out
 
