@@ -23,7 +23,7 @@ import numpy as np
 import pytest
 
 from tests.test_gpu_parity import TOL, _check, _operands
-from tests.util import csr, ragged, rel_inf
+from tests.util import csr, ragged, range_edge_matrix, rel_inf
 from tilegen_amd import codegen as cg
 from tilegen_amd.codegen import Config
 from tilegen_amd.matrices import make_baseline
@@ -118,6 +118,24 @@ def test_hybrid_more_ranges_than_scratch(hip_ready):
           flush=True)
     out = _check("spmv", cfg, A, K=1, label="hybrid_past_scratch")
     _again_onto_nan("spmv", cfg, A, out)
+
+
+@pytest.mark.parametrize("cfg", HYBRID_TEST_SCHEDULES, ids=[schedule_id(c) for c in
+                                                           HYBRID_TEST_SCHEDULES])
+@pytest.mark.parametrize("kernel", ["spmv", "fused_spmv_axpy"])
+def test_hybrid_range_edges(kernel, cfg, hip_ready):
+    """Every hybrid schedule on rows placed at its own ranges' edges: rows just
+    under and over the long-row length, three long rows meeting one range, rows
+    on range boundaries, two-piece and four-piece rows."""
+    CH = Variant(kernel, cfg).gen.geometry.nnz_chunk
+    A = range_edge_matrix(CH, seed=CH)
+    lens = np.diff(A.indptr)
+    assert (lens == CH // 2 + 1).sum() >= 6 and (lens > 3 * CH).any()
+    assert (A.indptr[:-1][lens > CH // 2] % CH == 0).any()
+    print("[gpu] hybrid edges %s %s CH=%d rows=%d nnz=%d" % (kernel, cfg.short(), CH,
+                                                            A.shape[0], A.nnz), flush=True)
+    out = _check(kernel, cfg, A, K=1, label="range_edges")
+    _again_onto_nan(kernel, cfg, A, out)
 
 
 def test_merge_path_agrees_with_row_tiles(hip_ready):

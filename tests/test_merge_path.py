@@ -28,7 +28,7 @@ import math
 import numpy as np
 import pytest
 
-from tests.util import ragged
+from tests.util import ragged, range_edge_matrix
 from tilegen_amd import codegen as cg
 from tilegen_amd.codegen import Config
 from tilegen_amd.matrices import make_baseline
@@ -329,12 +329,13 @@ def test_row_search_with_empty_rows_everywhere():
         assert lens[r] > 0 and rs <= t < re and (rs, re) == (ip[r], ip[r + 1])
 
 
-@pytest.mark.parametrize("CH", [128, 512, 2048])
+@pytest.mark.parametrize("CH", [128, 512, 1536, 2048])
 def test_ranges_list_every_long_row_meeting_them(CH):
     """The rows a range lists are exactly the rows longer than CH / 2 that meet
-    [p0, p1), with their bounds, and never more than 3 of them."""
+    [p0, p1), with their bounds, and never more than 3 of them; also on rows
+    placed at the ranges' own edges (the GPU test's matrix)."""
     LH = CH // 2
-    for label, A in _cases():
+    for label, A in list(_cases()) + [("range_edges", range_edge_matrix(CH, seed=CH))]:
         ip = np.asarray(A.indptr, dtype=np.int64)
         M, nnz = A.shape[0], int(ip[-1])
         lens = np.diff(ip)

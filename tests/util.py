@@ -48,6 +48,53 @@ def ragged(seed: int, rows: int, cols: int, max_len: int, empty_every: int = 0,
     return sp.csr_matrix((data, indices, indptr), shape=(rows, cols))
 
 
+def range_edge_matrix(CH: int, seed: int = 0):
+    """Rows at the edges of the hybrid range logic for ranges of CH nonzeros
+    (long rows: over LH = CH / 2): lengths LH (not long), LH + 1, three LH + 1
+    rows in a row (the most that can meet one range), CH and CH + 1, a row of
+    several ranges, rows starting and ending exactly on range boundaries (short
+    filler rows align them), with short and empty rows between."""
+    rng = np.random.default_rng(seed)
+    LH = CH // 2
+    lens = []
+
+    def pos():
+        return int(sum(lens))
+
+    def align_to(mult, off=0):
+        # short filler rows (at most 3 nonzeros each) up to the next position
+        # congruent to off modulo mult
+        gap = (off - pos()) % mult
+        while gap > 0:
+            k = min(3, gap)
+            lens.append(k)
+            gap -= k
+
+    for L in (LH, LH + 1, 0, 2, LH + 1, LH + 1, LH + 1, 1, 2 * LH - 1, CH, 0, CH + 1):
+        lens.append(L)
+        lens.extend(int(v) for v in rng.integers(0, 4, size=3))
+    align_to(CH)
+    lens.append(LH + 1)           # starts on a range boundary
+    align_to(CH, off=CH - (LH + 1))
+    lens.append(LH + 1)           # ends on a range boundary
+    align_to(CH, off=CH // 4)
+    lens.append(3 * CH + 7)       # four pieces
+    lens.append(LH + 2)
+    align_to(CH, off=CH - 1)
+    lens.append(CH + 2)           # two pieces, one nonzero in the first range
+    lens.extend(int(v) for v in rng.integers(0, 4, size=5))
+    lens.append(LH + 1)           # the last row reaches nnz
+    rows = len(lens)
+    cols = 4 * CH + 16
+    indptr = np.zeros(rows + 1, dtype=np.int64)
+    np.cumsum(lens, out=indptr[1:])
+    indices = np.empty(int(indptr[-1]), dtype=np.int64)
+    for r, L in enumerate(lens):
+        if L:
+            indices[indptr[r]:indptr[r + 1]] = np.sort(rng.choice(cols, size=L, replace=False))
+    return csr(rows, cols, indptr, indices, rng.uniform(-1, 1, size=indices.size))
+
+
 def rel_inf(out, ref) -> float:
     out = np.asarray(out, dtype=np.float64).ravel()
     ref = np.asarray(ref, dtype=np.float64).ravel()

@@ -729,6 +729,12 @@ def hybrid_chunk(low: Lowering) -> int:
     return 2 * min(low.block_size, 1024) * max(1, low.unroll)
 
 
+def hybrid_long(low: Lowering) -> int:
+    """Rows longer than this are summed by the long-row workgroups of hybrid
+    tiles: half a range, so at most 3 of them meet one range."""
+    return hybrid_chunk(low) // 2
+
+
 def _check_hip_schedule(plan: Plan, low: Lowering) -> None:
     B, tpr = low.block_size, low.threads_per_row
     if B % WAVE or B <= 0 or B > 1024:
@@ -1270,7 +1276,7 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         R = (TR + SLOTS - 1) // SLOTS
     if hybrid:
         CH = hybrid_chunk(low)
-        LH = CH // 2  # at most 3 rows this long meet one range of CH nonzeros
+        LH = hybrid_long(low)
 
     if merge:
         w("const tg_i64 row_lim = %s;  // rows this launch writes" % bound)
