@@ -358,3 +358,42 @@ def test_matrices_without_nonzeros(kernel, hip_ready):
             assert np.array_equal(out, want), (kernel, cfg.short(), M)
             r = verify(kernel, cfg, A, backend="hip", K=8)
             assert r.ok, r.message
+
+
+def _nonfinite_cases():
+    from tilegen_amd.schedules import HYBRID_TEST_SCHEDULES, MERGE_TEST_SCHEDULES, TUNED
+    rows = [Config(tile_size=32, threads_per_row=1, unroll=1, block_size=128),
+            Config(tile_size=64, threads_per_row=4, unroll=4, block_size=256),
+            Config(tile_size=16, threads_per_row=8, unroll=2, block_size=128),
+            Config(tile_size=8, threads_per_row=64, unroll=2, block_size=256)]
+    return rows + MERGE_TEST_SCHEDULES[:3] + HYBRID_TEST_SCHEDULES[:3] + [TUNED["c3a"],
+                                                                       TUNED["c3b"]]
+
+
+@pytest.mark.parametrize("cfg", _nonfinite_cases(), ids=[schedule_id(c) for c in
+                                                          _nonfinite_cases()])
+@pytest.mark.parametrize("kernel", ["spmv", "fused_spmv_axpy"])
+def test_nonfinite_x_reaches_only_rows_that_use_it(kernel, cfg, hip_ready):
+    """x[0] = NaN and x[5] = +Inf.  Lanes past a row's end gather x[0] so that
+    every gather of a step is issued before any is used; their products must
+    be dropped, not multiplied by zero (0 * NaN is NaN).  So exactly the rows
+    that reference column 0 or 5 are non-finite, with SciPy's NaN/Inf pattern,
+    and every other row meets the bar."""
+    A = ragged(41, 3000, 2000, 40, empty_every=9,
+               long_rows=[(17, 1900), (1500, 1300), (2999, 700)])
+    ops = _operands(kernel, A, 1)
+    x = ops["x"].copy()
+    x[0], x[5] = np.nan, np.inf
+    ops["x"] = x
+    out = Variant(kernel, cfg).run(A, **ops)
+    sci = _reference(kernel, A, (x, ops["w"], ops["B"], ops["U"], ops["V"],
+                                 ops["alpha"], ops["beta"]))
+    uses = np.zeros(A.shape[0], dtype=bool)
+    coo = A.tocoo()
+    uses[coo.row[(coo.col == 0) | (coo.col == 5)]] = True
+    assert 0 < uses.sum() < A.shape[0] // 2
+    assert np.array_equal(np.isnan(out), np.isnan(sci)), cfg.short()
+    assert np.array_equal(np.isinf(out), np.isinf(sci)), cfg.short()
+    assert np.array_equal(~np.isfinite(sci), uses)  # the rows that use them, and only those
+    fin = np.isfinite(sci)
+    assert rel_inf(out[fin], sci[fin]) <= TOL, cfg.short()
