@@ -67,7 +67,7 @@ def _parse_config(text: str):
     vals = {}
     for part in text.replace(",", "/").split("/"):
         part = part.strip()
-        if part in ("nnz", "rows", "hybrid"):  # what a tile holds (see Config.balance)
+        if part in ("nnz", "rows", "hybrid", "stream"):  # what a tile holds (Config.balance)
             vals["balance"] = part
             continue
         for key, name in (("TPR", "threads_per_row"), ("T", "tile_size"), ("U", "unroll"),
@@ -368,7 +368,7 @@ def main(argv=None) -> int:
     ap.add_argument("--config", default=None,
                     help="schedule override for the headline case, e.g. T128/TPR8/U2/V1/B256 "
                          "(append /nnz for merge-path windows, /hybrid for long-row "
-                         "workgroups)")
+                         "workgroups, /stream for equal nonzero ranges)")
     ap.add_argument("--case-iters", type=int, default=200,
                     help="event-timed launches per config under 'cases'")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,

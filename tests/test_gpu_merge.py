@@ -1,12 +1,14 @@
-"""GPU parity of the merge-path (balance "nnz") and hybrid (balance
-"hybrid") SpMV and fused_spmv_axpy.
+"""GPU parity of the merge-path (balance "nnz"), hybrid (balance "hybrid") and
+stream (balance "stream") SpMV and fused_spmv_axpy.
 
 Each workgroup takes an equal share of rows plus nonzeros, finds its first and
 last rows with a search of the row pointers, sums the rows that begin in its
 share whole, and adds its piece of any row longer than a share to the scratch
 the last piece reads back.  Hybrid tiles keep row tiles but leave rows longer
 than half a nonzero range to workgroups that each take one range, with the
-same piece combine.  The matrices put that logic at its edges: no
+same piece combine.  Stream ranges give every workgroup one equal range of
+nonzeros and the rows that end in it, and combine the rows cut at range edges
+the same way.  The matrices put that logic at its edges: no
 nonzeros, one row, rows ending exactly at the last nonzero, a row spanning
 hundreds of windows (more than one wave of pieces to combine), long first and
 last rows, mostly empty rows, power-law and dense-row patterns, and more
@@ -27,7 +29,8 @@ from tests.util import csr, ragged, range_edge_matrix, rel_inf
 from tilegen_amd import codegen as cg
 from tilegen_amd.codegen import Config
 from tilegen_amd.matrices import make_baseline
-from tilegen_amd.schedules import HYBRID_TEST_SCHEDULES, MERGE_TEST_SCHEDULES, schedule_id
+from tilegen_amd.schedules import (HYBRID_TEST_SCHEDULES, MERGE_TEST_SCHEDULES,
+                                   STREAM_TEST_SCHEDULES, schedule_id)
 from tilegen_amd.variant import Variant
 
 pytestmark = pytest.mark.gpu
@@ -57,8 +60,10 @@ def _again_onto_nan(kernel, cfg, A, first):
     assert np.array_equal(out, first)
 
 
-@pytest.mark.parametrize("cfg", MERGE_TEST_SCHEDULES + HYBRID_TEST_SCHEDULES,
-                         ids=[schedule_id(c) for c in MERGE_TEST_SCHEDULES + HYBRID_TEST_SCHEDULES])
+_BALANCED = MERGE_TEST_SCHEDULES + HYBRID_TEST_SCHEDULES + STREAM_TEST_SCHEDULES
+
+
+@pytest.mark.parametrize("cfg", _BALANCED, ids=[schedule_id(c) for c in _BALANCED])
 @pytest.mark.parametrize("kernel", ["spmv", "fused_spmv_axpy"])
 def test_merge_path_matches_oracle(kernel, cfg, hip_ready):
     for label, A in _cases().items():
@@ -68,7 +73,7 @@ def test_merge_path_matches_oracle(kernel, cfg, hip_ready):
         _again_onto_nan(kernel, cfg, A, out)
 
 
-@pytest.mark.parametrize("balance", ["nnz", "hybrid"])
+@pytest.mark.parametrize("balance", ["nnz", "hybrid", "stream"])
 def test_zero_rows_launch_nothing(balance, hip_ready):
     """No rows and no nonzeros make an empty grid: the launcher returns before
     any kernel runs, and the next launch of the same variant is unaffected."""
@@ -139,29 +144,30 @@ def test_hybrid_range_edges(kernel, cfg, hip_ready):
 
 
 def test_merge_path_agrees_with_row_tiles(hip_ready):
-    """The same schedule with row tiles and with merge-path windows: both meet
-    the bar on the BASELINE skewed cases at a tenth of their size, and agree
-    with each other to it."""
+    """The same schedule with row tiles, merge-path windows, hybrid tiles and
+    stream ranges: all meet the bar on the BASELINE skewed cases at a tenth of
+    their size, and agree with each other to it."""
     for case_id, base in (("c3a", (64, 8, 2, 512)), ("c3b", (32, 32, 2, 1024))):
         A = make_baseline(case_id, scale=0.1)
         ops = _operands("spmv", A, 1)
         T, tpr, U, B = base
         rows = Variant("spmv", Config(tile_size=T, threads_per_row=tpr, unroll=U,
                                       block_size=B)).run(A, **ops)
-        for balance in ("nnz", "hybrid"):
+        for balance in ("nnz", "hybrid", "stream"):
             other = Variant("spmv", Config(tile_size=T, threads_per_row=tpr, unroll=U,
                                            block_size=B, balance=balance)).run(A, **ops)
             assert rel_inf(other, rows) <= TOL, (case_id, balance)
 
 
-@pytest.mark.parametrize("cfg", MERGE_TEST_SCHEDULES[:2] + HYBRID_TEST_SCHEDULES[:2],
+@pytest.mark.parametrize("cfg", MERGE_TEST_SCHEDULES[:2] + HYBRID_TEST_SCHEDULES[:2] +
+                         STREAM_TEST_SCHEDULES[:2],
                          ids=[schedule_id(c) for c in MERGE_TEST_SCHEDULES[:2] +
-                              HYBRID_TEST_SCHEDULES[:2]])
+                              HYBRID_TEST_SCHEDULES[:2] + STREAM_TEST_SCHEDULES[:2]])
 @pytest.mark.parametrize("kernel", ["spmv", "fused_spmv_axpy"])
 def test_verify_api_with_balance(kernel, cfg, hip_ready, tmp_path):
-    """The reference's verify() on its 257 x 257 test matrix with merge-path
-    and hybrid schedules: the reference tolerance, the 1e-10 normwise bar and
-    indptr/indices untouched."""
+    """The reference's verify() on its 257 x 257 test matrix with merge-path,
+    hybrid and stream schedules: the reference tolerance, the 1e-10 normwise bar
+    and indptr/indices untouched."""
     from tests.util import mixed_257
     from tilegen_amd.verify import verify
     r = verify(kernel, cfg, mixed_257(), backend="hip", workdir=str(tmp_path), K=8)
@@ -172,19 +178,21 @@ def test_verify_api_with_balance(kernel, cfg, hip_ready, tmp_path):
 
 
 def test_tune_with_balance_candidates(hip_ready, tmp_path):
-    """tune() times and verifies merge-path and hybrid candidates beside row
-    tiles on a skewed matrix; every candidate it ran is correct and the winner
-    is one of them."""
+    """tune() times and verifies merge-path, hybrid and stream candidates beside
+    row tiles on a skewed matrix; every candidate it ran is correct and the
+    winner is one of them."""
     from tilegen_amd.autotune import tune
     A = make_baseline("c3a", scale=0.05)
-    inc = [MERGE_TEST_SCHEDULES[1], HYBRID_TEST_SCHEDULES[1], HYBRID_TEST_SCHEDULES[0]]
+    inc = [MERGE_TEST_SCHEDULES[1], HYBRID_TEST_SCHEDULES[1], HYBRID_TEST_SCHEDULES[0],
+           STREAM_TEST_SCHEDULES[0]]
     res = tune("spmv", A, budget=len(inc) + 1, mode="random", backend="hip", include=inc,
                iters=5, warmup=2, workdir=str(tmp_path))
     ran = [r for r in res["records"] if r.get("ms_median") is not None]
     assert len(ran) == len(inc) + 1
     assert all(r["ok"] for r in ran)
     assert res["winner"] in [r["config"] for r in ran]
-    assert {r["config"].get("balance", "rows") for r in ran} == {"rows", "nnz", "hybrid"}
+    assert {r["config"].get("balance", "rows") for r in ran} == {"rows", "nnz", "hybrid",
+                                                                 "stream"}
 
 
 def _device_set(A, ops, out_len):
@@ -199,8 +207,8 @@ def _device_set(A, ops, out_len):
 
 @pytest.mark.parametrize("case_id", ["c3a", "c3b"])
 def test_scratch_variant_on_two_streams(case_id, hip_ready):
-    """The tuned hybrid variants combine long-row pieces through one module
-    scratch per device.  Launches on two streams, enqueued back to back with no
+    """The tuned skewed-row variants (stream ranges on c3a, hybrid tiles on c3b)
+    combine row pieces through one module scratch per device.  Launches on two streams, enqueued back to back with no
     host synchronization in between (and two more on the null stream), are
     ordered by the launcher, so every output equals a serial launch's bits."""
     from tilegen_amd import runtime as rt
@@ -245,3 +253,35 @@ def _kernel(name, cfg):
     from tilegen_amd import passes
     from tilegen_amd.dsl import standard_kernels
     return passes.run_pipeline(standard_kernels()[name], cfg, backend="hip")
+
+
+def _stream_scratch_matrix(CH):
+    """About 75000 ranges of CH = 64 nonzeros: a long row near the top (cut into
+    pieces inside the scratch), one straddling the last range with slots, and
+    one beginning past it."""
+    rows, max_len, seed = 160_000, 60, 41
+    lengths = np.random.default_rng(seed).integers(0, max_len + 1, size=rows)
+    lengths[10] = 700
+    starts = np.concatenate([[0], np.cumsum(lengths)])
+    edge = int(np.searchsorted(starts, cg.MERGE_CAP * CH - 300, side="right")) - 1
+    return ragged(seed, rows, 4096, max_len,
+                  long_rows=[(10, 700), (edge, 900), (rows - 60, 900)]), edge
+
+
+def test_stream_more_ranges_than_scratch(hip_ready):
+    """More ranges than the 65536 with scratch slots: the long row near the top
+    is combined through the scratch; the row straddling the last range with
+    slots and the row beginning past it are summed whole, with their own loads,
+    by the range each begins in."""
+    cfg = Config(tile_size=64, threads_per_row=1, unroll=1, block_size=64, balance="stream")
+    CH = Variant("spmv", cfg).gen.geometry.nnz_chunk
+    A, edge = _stream_scratch_matrix(CH)
+    rows, ip = A.shape[0], A.indptr
+    assert CH == 64 and -(-A.nnz // CH) > cg.MERGE_CAP
+    assert ip[10] // CH < (ip[11] - 1) // CH < cg.MERGE_CAP
+    assert ip[edge] // CH < cg.MERGE_CAP <= (ip[edge + 1] - 1) // CH
+    assert cg.MERGE_CAP <= ip[rows - 60] // CH < (ip[rows - 59] - 1) // CH
+    print("[gpu] stream scratch capacity rows=%d nnz=%d ranges=%d" % (rows, A.nnz, -(-A.nnz // CH)),
+          flush=True)
+    out = _check("spmv", cfg, A, K=1, label="stream_past_scratch")
+    _again_onto_nan("spmv", cfg, A, out)

@@ -361,13 +361,14 @@ def test_matrices_without_nonzeros(kernel, hip_ready):
 
 
 def _nonfinite_cases():
-    from tilegen_amd.schedules import HYBRID_TEST_SCHEDULES, MERGE_TEST_SCHEDULES, TUNED
+    from tilegen_amd.schedules import (HYBRID_TEST_SCHEDULES, MERGE_TEST_SCHEDULES,
+                                       STREAM_TEST_SCHEDULES, TUNED)
     rows = [Config(tile_size=32, threads_per_row=1, unroll=1, block_size=128),
             Config(tile_size=64, threads_per_row=4, unroll=4, block_size=256),
             Config(tile_size=16, threads_per_row=8, unroll=2, block_size=128),
             Config(tile_size=8, threads_per_row=64, unroll=2, block_size=256)]
-    return rows + MERGE_TEST_SCHEDULES[:3] + HYBRID_TEST_SCHEDULES[:3] + [TUNED["c3a"],
-                                                                       TUNED["c3b"]]
+    return (rows + MERGE_TEST_SCHEDULES[:3] + HYBRID_TEST_SCHEDULES[:3] +
+            STREAM_TEST_SCHEDULES[:3] + [TUNED["c3a"], TUNED["c3b"]])
 
 
 @pytest.mark.parametrize("cfg", _nonfinite_cases(), ids=[schedule_id(c) for c in

@@ -63,8 +63,8 @@ BASELINE = Config(tile_size=32, threads_per_row=1, unroll=1, vector_width=1, blo
 
 _WAVE = 64
 _LDS_LIMIT = 160 * 1024  # LDS per CU on gfx950, all of which one workgroup may take
-# kernels whose schedules also come with merge-path windows and hybrid tiles
-# (Config.balance)
+# kernels whose schedules also come with merge-path windows, hybrid tiles and
+# stream ranges (Config.balance)
 MERGE_KERNELS = ("spmv", "fused_spmv_axpy")
 ROTATE_BYTES = 640 << 20
 
@@ -131,6 +131,8 @@ def illegal_reason_for(kernel: str, cfg: Config, K: int = 8) -> Optional[str]:
     r = illegal_reason(cfg)
     if r is not None:
         return r
+    if cfg.balance == "stream" and _stream_reason(cfg) is not None:
+        return _stream_reason(cfg)
     if kernel in ("spmv", "fused_spmv_axpy") and cfg.vector_width != 1:
         return "vector_width has no effect on %s (the vectorize pass drops it)" % kernel
     if kernel == "spmm" and cfg.threads_per_row * cfg.vector_width > max(_WAVE, 2 * K):
@@ -170,7 +172,21 @@ def enumerate_configs(kernel: Optional[str] = None, K: int = 8
         rows = list(out)
         for balance in ("nnz", "hybrid"):
             out += [(dataclasses.replace(c, balance=balance), r) for c, r in rows]
+        # and with stream ranges, which do not use the tile size: each (TPR, U, B)
+        # once, at the smallest legal tile
+        out += [(dataclasses.replace(c, balance="stream"),
+                 r if r is not None else _stream_reason(c)) for c, r in rows
+                if c.tile_size == c.block_size // c.threads_per_row]
     return out
+
+
+def _stream_reason(cfg: Config) -> Optional[str]:
+    """Stream ranges stage their products in LDS: block x unroll nonzeros."""
+    from .codegen import STREAM_MAX_CHUNK
+    if cfg.block_size * cfg.unroll > STREAM_MAX_CHUNK:
+        return "stream range of %d nonzeros exceeds %d" % (cfg.block_size * cfg.unroll,
+                                                          STREAM_MAX_CHUNK)
+    return None
 
 
 def legal_configs(kernel: Optional[str] = None, K: int = 8) -> List[Config]:
@@ -341,7 +357,7 @@ def _candidate_configs(kernel: str, K: int, budget: int, mode: str, rng: random.
         best = out[0]
         steps = [(key, value) for key in SEARCH_SPACE for value in SEARCH_SPACE[key]]
         if kernel in MERGE_KERNELS and backend != "cpu":
-            steps += [("balance", "nnz"), ("balance", "hybrid")]
+            steps += [("balance", "nnz"), ("balance", "hybrid"), ("balance", "stream")]
         for key, value in steps:
             add(Config(**{**best.to_dict(), key: value}))
             if len(out) >= budget:

@@ -22,10 +22,11 @@ backend "hip"
         whose first step is issued for every row before any gather, so each
         wave keeps several rows of loads in flight.  Config.balance picks what
         a tile holds: T rows ("rows"), an equal merge-path window of rows plus
-        nonzeros ("nnz"), or T rows with the rows longer than B*U nonzeros
-        left to workgroups over equal nonzero ranges ("hybrid"); rows cut
-        across workgroups are combined in a fixed order through module
-        scratch.
+        nonzeros ("nnz"), T rows with the rows longer than B*U nonzeros
+        left to workgroups over equal nonzero ranges ("hybrid"), or an equal
+        range of B*U nonzeros whose products are staged in LDS and summed
+        there for the rows that end in the range ("stream"); rows cut across
+        workgroups are combined in a fixed order through module scratch.
     row_dense_out (spmm)
         ThreadsPerRow(k) lanes per output row spread over the K columns,
         Vectorize(2) = 128-bit loads of B rows and stores of C, Unroll(u) =
@@ -95,10 +96,12 @@ class Config:
     tile_size T (rows per workgroup), threads_per_row TPR, unroll U,
     vector_width V, block_size B (lanes per workgroup).  ``balance`` is what
     a tile holds on the HIP backend: ``"rows"`` (T consecutive rows),
-    ``"nnz"`` (an equal share of rows plus nonzeros, about T rows' worth) or
+    ``"nnz"`` (an equal share of rows plus nonzeros, about T rows' worth),
     ``"hybrid"`` (T rows, with rows past a length threshold left to extra
-    workgroups that each take an equal range of nonzeros); the last two are for
-    SpMV-shaped kernels (see ``_hip_scalar_reduce``).  It has no counterpart in
+    workgroups that each take an equal range of nonzeros) or ``"stream"`` (an
+    equal range of B*U nonzeros and the rows that end in it; T is not used);
+    the last three are for SpMV-shaped kernels (see ``_hip_scalar_reduce`` and
+    ``_hip_stream_reduce``).  It has no counterpart in
     the reference and is left out of ``to_dict``/``hash`` at its default, so
     every reference schedule keeps its name.
     """
@@ -186,17 +189,22 @@ def _lowering(kernel: Kernel) -> Lowering:
 class LaunchGeometry:
     """Grid rule of a HIP variant: ``grid = ceil(rows / rows_per_block)``,
     plus ``ceil(nnz / nnz_chunk)`` workgroups ahead of those when
-    ``nnz_chunk`` is set (hybrid tiles' long-row workgroups)."""
+    ``nnz_chunk`` is set (hybrid tiles' long-row workgroups).  With
+    ``stream`` the grid is ``ceil(nnz / nnz_chunk)`` alone, at least one
+    workgroup when there are rows (they are written even without nonzeros)."""
 
     rows_per_block: int
     block: int
     lds_bytes: int
     rows_symbol: str = "M"
     nnz_chunk: int = 0
+    stream: bool = False
 
     def grid(self, rows: int, nnz: int = 0) -> int:
         if rows <= 0:
             return 0
+        if self.stream:
+            return max(1, (int(nnz) + self.nnz_chunk - 1) // self.nnz_chunk)
         g = (int(rows) + self.rows_per_block - 1) // self.rows_per_block
         if self.nnz_chunk and nnz > 0:
             g += (int(nnz) + self.nnz_chunk - 1) // self.nnz_chunk
@@ -207,6 +215,8 @@ class LaunchGeometry:
              "lds_bytes": self.lds_bytes, "rows_symbol": self.rows_symbol}
         if self.nnz_chunk:
             d["nnz_chunk"] = self.nnz_chunk
+        if self.stream:
+            d["stream"] = True
         return d
 
 
@@ -710,6 +720,10 @@ def launch_geometry(plan: Plan, low: Lowering) -> LaunchGeometry:
     if plan.kind == "sparse_out":
         return LaunchGeometry(low.tile if low.tiled else slots, B, 0, plan.row_extent)
     rows = low.tile if low.tiled else slots
+    if plan.kind == "scalar_reduce" and low.tiled and low.balance == "stream":
+        CH, RB = stream_chunk(low), stream_batch(low)
+        lds = 8 * CH + 8 * (RB + 1) + 4 * RB + 8 * 6 + 4
+        return LaunchGeometry(1, B, lds, plan.row_extent, CH, stream=True)
     lds = 8 * (rows + 1) if (plan.kind == "scalar_reduce" and low.tiled) else 0
     chunk = hybrid_chunk(low) if (plan.kind == "scalar_reduce" and low.tiled
                                   and low.balance == "hybrid") else 0
@@ -718,9 +732,28 @@ def launch_geometry(plan: Plan, low: Lowering) -> LaunchGeometry:
 
 def module_scratch(plan: Plan, low: Lowering) -> bool:
     """Whether the variant's module keeps row-piece partials in its scratch
-    (merge-path windows and hybrid tiles), so that launches of it must not
-    overlap on one device."""
-    return plan.kind == "scalar_reduce" and low.tiled and low.balance in ("nnz", "hybrid")
+    (merge-path windows, hybrid tiles and stream ranges), so that launches of it
+    must not overlap on one device."""
+    return (plan.kind == "scalar_reduce" and low.tiled
+            and low.balance in ("nnz", "hybrid", "stream"))
+
+
+# Stream ranges: at most this many nonzeros per workgroup (their products are
+# staged in LDS, 8 bytes each)
+STREAM_MAX_CHUNK = 8192
+
+
+def stream_chunk(low: Lowering) -> int:
+    """Nonzeros per workgroup of the stream form: one pass of the whole
+    workgroup, U nonzeros per lane."""
+    return min(low.block_size, 1024) * max(1, low.unroll)
+
+
+def stream_batch(low: Lowering) -> int:
+    """Row pointers a stream workgroup stages at a time: a range of CH
+    nonzeros ends at most CH non-empty rows, so one batch holds all of them
+    unless empty rows pile up."""
+    return min(1024, max(64, stream_chunk(low)))
 
 
 def hybrid_chunk(low: Lowering) -> int:
@@ -752,6 +785,9 @@ def _check_hip_schedule(plan: Plan, low: Lowering) -> None:
         raise ValueError("balance '%s' needs a tiled kernel that reduces over each row "
                          "(SpMV-shaped); %s %s" % (low.balance, plan.kind,
                                                    "untiled" if not low.tiled else ""))
+    if low.balance == "stream" and stream_chunk(low) > STREAM_MAX_CHUNK:
+        raise ValueError("stream ranges hold at most %d nonzeros (block_size x unroll), got %d"
+                         % (STREAM_MAX_CHUNK, stream_chunk(low)))
 
 
 def _long_row_test(length: str, long_: int, huge: int) -> str:
@@ -1180,6 +1216,219 @@ def _hybrid_ranges(w: _W, plan: Plan, step, out_name: str, B: int, U: int, ALIGN
     w.close()
 
 
+def _hip_stream_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeometry,
+                       out_name: str, pre: _W, scratch_arg: bool = False) -> None:
+    """y[row] = final(sum over the row's nonzeros of value_expr), one equal range of
+    nonzeros per workgroup (``balance == "stream"``).
+
+    Workgroup e takes the nonzeros [p0, p1) = [e CH, (e+1) CH), CH = B U, and
+    owns the rows [ra, rb): ra is the row holding p0 (0 for e = 0, so the first
+    workgroup also owns the empty rows ahead of the first nonzero) and rb the
+    row holding p1 (M for the last workgroup).  Every row belongs to exactly one
+    workgroup: the one its last nonzero lies in (for an empty row, the one its
+    position lies in).
+
+    1. Every lane loads its U nonzeros (128-bit (index, value) pairs, coalesced
+       over the workgroup), then waves 0 and 1 find ra and rb with
+       ``tg_mp_row`` while those loads are in flight.  The operands are
+       gathered and the products staged in LDS.  Nothing here depends on row
+       lengths, so the matrix streams at full width however skewed it is.
+    2. After one barrier, the row pieces cut at range edges are committed
+       first, so that their atomic round trips overlap the row sums: wave 0
+       the last piece of row ra when it began in an earlier range, wave 1 this
+       range's piece of row rb.  ``tg_mp_commit`` adds the pieces in range
+       order.  A row with a piece in a range past the scratch's MERGE_CAP
+       ranges is summed whole, with its own loads, by the range it begins in.
+    3. The owned rows' pointers are staged RB at a time, and each row is summed
+       from the staged products by a lane group of TPR lanes (DPP); rows over
+       64 nonzeros are listed and summed by one wave each.
+    """
+    if not _value_row_free(plan):
+        raise ValueError("stream ranges need a per-nonzero value that reads only the sparse "
+                         "value and the gathered operand")
+    B = geo.block
+    TPR = max(1, low.threads_per_row)
+    U = max(1, low.unroll)
+    CH, RB = stream_chunk(low), stream_batch(low)
+    WAVES = B // WAVE
+    SLOTS = B // TPR
+    row = plan.row_idx.name
+    col = plan.col_idx.name
+    gathered = _gather_operand(plan)
+
+    def pos(u: int) -> str:
+        """Position in the range of lane threadIdx.x's u-th nonzero."""
+        if U % 2 == 0:
+            return "2 * (%d + (int)threadIdx.x)%s" % ((u // 2) * B, " + 1" if u % 2 else "")
+        return "%d + (int)threadIdx.x" % (u * B)
+
+    def gather(col_text: str) -> str:
+        return _cexpr(gathered, _Env({row: "row", col: col_text}, p="pq"))
+
+    def store(acc: str, row_text: str) -> None:
+        w("const tg_i64 row = %s;" % row_text)
+        env = _Env({row: "row"}, acc=acc)
+        w("__builtin_nontemporal_store(%s, %s + %s);" % (
+            _cexpr(plan.final_expr, env), out_name, _offset(plan.out_tensor, plan.out.indices, env)))
+
+    _merge_decls(pre, scratch_arg)
+    if not scratch_arg:
+        w("unsigned long long* const tg_part = tg_mp_part;")
+    w("const tg_i64 row_end = %s;  // rows written" % bound)
+    w("const tg_i64 n_rows = %s;  // rows of the matrix" % plan.row_extent)
+    w("__shared__ double s_prod[%d];  // this range's products" % CH)
+    w("__shared__ tg_i64 s_ptr[%d];  // owned rows' pointers, %d rows at a time" % (RB + 1, RB))
+    w("__shared__ tg_i64 s_b[6];  // the rows holding p0 and p1: row, start, end")
+    w("__shared__ int s_long[%d];  // staged rows over 64 nonzeros" % RB)
+    w("__shared__ int s_nlong;")
+    w("const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);")
+    w("const int l = threadIdx.x & 63;")
+    w("const tg_i64 e = blockIdx.x;")
+    w("const tg_i64 p0 = e * %d, p1 = p0 + %d < nnz ? p0 + %d : nnz;" % (CH, CH, CH))
+    w("const int cnt = (int)(p1 - p0);  // nonzeros in this range")
+    w("// 1. this range's indices and values, every load issued before any is used")
+    w("tg_i64 ci[%d]; double cv[%d];" % (U, U))
+    if U % 2 == 0:
+        w("// 128-bit (index, value) pair loads need 16-byte aligned bases; a caller's")
+        w("// sub-buffer may be only 8-byte aligned, which takes the per-element loads")
+        w("const bool pair_ok = ((((unsigned long long)indices) | "
+          "((unsigned long long)data)) & 15) == 0;")
+        for u in range(0, U, 2):
+            w.open("")
+            w("const int q = %s;" % pos(u))
+            w.open("if (pair_ok && q + 1 < cnt)")
+            w("const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + p0 + q));")
+            w("const tg_f64x2 b = __builtin_nontemporal_load((const tg_f64x2*)(data + p0 + q));")
+            w("ci[%d] = a.x; ci[%d] = a.y; cv[%d] = b.x; cv[%d] = b.y;" % (u, u + 1, u, u + 1))
+            w.close()
+            w.open("else")
+            for d in (0, 1):
+                w("ci[%d] = q + %d < cnt ? __builtin_nontemporal_load(indices + p0 + q + %d) : 0;"
+                  % (u + d, d, d))
+                w("cv[%d] = q + %d < cnt ? __builtin_nontemporal_load(data + p0 + q + %d) : 0.0;"
+                  % (u + d, d, d))
+            w.close()
+            w.close()
+    else:
+        for u in range(U):
+            w.open("")
+            w("const int q = %s;" % pos(u))
+            w("ci[%d] = q < cnt ? __builtin_nontemporal_load(indices + p0 + q) : 0;" % u)
+            w("cv[%d] = q < cnt ? __builtin_nontemporal_load(data + p0 + q) : 0.0;" % u)
+            w.close()
+    w("if (threadIdx.x == 0) s_nlong = 0;")
+    w("// the rows holding p0 (wave 0) and p1 (wave 1), searched while the loads are in")
+    w("// flight; the first range owns the rows from 0, the last the rows up to M")
+    w("#pragma unroll 1")
+    w.open("for (int k = wv; k < 2; k += %d)" % WAVES)
+    w("const tg_i64 P = k == 0 ? p0 : p1;")
+    w("tg_i64 r = n_rows, rs = nnz, re = nnz;")
+    w("if (k == 0 && e == 0) { r = 0; rs = 0; re = 0; }")
+    w("else if (P < nnz) r = tg_mp_row(indptr, n_rows, P, nnz, &rs, &re);")
+    w("if (l == 0) { s_b[3 * k] = r; s_b[3 * k + 1] = rs; s_b[3 * k + 2] = re; }")
+    w.close()
+    w("// the operands (positions past the range gather nothing) and the products, in LDS")
+    w("double xv[%d];" % U)
+    for u in range(U):
+        w("{ const int q = %s; xv[%d] = q < cnt ? %s : 0.0; }" % (pos(u), u, gather("ci[%d]" % u)))
+    for u in range(U):
+        w("{ const int q = %s; if (q < cnt) s_prod[q] = %s; }"
+          % (pos(u), _value_with(plan, "cv[%d]" % u, "xv[%d]" % u, row, "ci[%d]" % u)))
+    w("__syncthreads();")
+    w("const tg_i64 ra = s_b[0], ra_s = s_b[1], ra_e = s_b[2];")
+    w("const tg_i64 rb = s_b[3], rb_s = s_b[4], rb_e = s_b[5];")
+    w("// row ra began in an earlier range, so this range holds its last piece")
+    w("const bool ra_cut = e > 0 && ra < rb && ra_s < p0;")
+    w("// 2. the pieces cut at range edges first, so that their atomics overlap the row sums")
+    w.open("if (wv == 0 && ra_cut)")
+    w("const tg_i64 ef = ra_s / %d, el = (ra_e - 1) / %d;  // the ranges it spans" % (CH, CH))
+    w.open("if (el < %d)" % MERGE_CAP)
+    w("const int en = (int)(ra_e - p0);")
+    w("double t = 0.0;")
+    w("#pragma unroll 1")
+    w("for (int q = l; q < en; q += 64) t += s_prod[q];")
+    w("t = tg_segsum<64>(t);")
+    w("double tot = t;")
+    w.open("if (tg_mp_commit(tg_part, e, ef, el, t, &tot) && l == 0 && ra < row_end)")
+    store("tot", "ra")
+    w.close()
+    w.close()
+    w("// otherwise the range it begins in sums it whole (below)")
+    w.close()
+    w.open("if (wv == %d && rb < n_rows && rb_s < p1)" % (1 if WAVES > 1 else 0))
+    w("const tg_i64 ef = rb_s / %d, el = (rb_e - 1) / %d;" % (CH, CH))
+    w.open("if (el < %d)" % MERGE_CAP)
+    w("const int st = (int)((rb_s > p0 ? rb_s : p0) - p0);")
+    w("double t = 0.0;")
+    w("#pragma unroll 1")
+    w("for (int q = st + l; q < cnt; q += 64) t += s_prod[q];")
+    w("t = tg_segsum<64>(t);")
+    w("double tot = t;")
+    w.open("if (tg_mp_commit(tg_part, e, ef, el, t, &tot) && l == 0 && rb < row_end)")
+    store("tot", "rb")
+    w.close()
+    w.close()
+    w.open("else if (ef == e)")
+    w("// a row reaching past the scratch's last range: summed whole by its first range")
+    w("double t = 0.0;")
+    w("#pragma unroll 1")
+    w.open("for (tg_i64 pq = rb_s + l; pq < rb_e; pq += 64)")
+    w("const tg_i64 cq = indices[pq];")
+    w("t += %s;" % _value_with(plan, "data[pq]", gather("cq"), row, "cq"))
+    w.close()
+    w("t = tg_segsum<64>(t);")
+    w.open("if (l == 0 && rb < row_end)")
+    store("t", "rb")
+    w.close()
+    w.close()
+    w.close()
+    w("// 3. the owned rows [ra, rb), %d row pointers at a time" % RB)
+    w("const int lane = threadIdx.x %% %d;" % TPR)
+    w("const int slot = threadIdx.x / %d;" % TPR)
+    w("#pragma unroll 1")
+    w.open("for (tg_i64 b0 = ra; b0 < rb; b0 += %d)" % RB)
+    w("const int nb = (int)(rb - b0 < %d ? rb - b0 : %d);" % (RB, RB))
+    w("for (int i = threadIdx.x; i <= nb; i += %d) s_ptr[i] = indptr[b0 + i];" % B)
+    w("__syncthreads();")
+    w("// rows of up to 64 nonzeros: one lane group each")
+    w("#pragma unroll 1")
+    w.open("for (int i = slot; i < nb; i += %d)" % SLOTS)
+    w("const tg_i64 rs = s_ptr[i], re = s_ptr[i + 1];")
+    w("const int st = (int)((rs > p0 ? rs : p0) - p0), en = (int)(re - p0);")
+    w("const bool mine = !(b0 + i == ra && ra_cut);  // a cut ra was committed above")
+    w("const bool own = mine && en - st <= 64;")
+    w("double acc = 0.0;")
+    w.open("if (own)")
+    w("#pragma unroll 1")
+    w("for (int q = st + lane; q < en; q += %d) acc += s_prod[q];" % TPR)
+    w.close()
+    w("if (mine && !own && lane == 0) s_long[atomicAdd(&s_nlong, 1)] = i;")
+    w("acc = tg_segsum<%d>(acc);" % TPR)
+    w.open("if (own && lane == 0 && b0 + i < row_end)")
+    store("acc", "b0 + i")
+    w.close()
+    w.close()
+    w("__syncthreads();")
+    w("// longer rows: one wave each")
+    w("const int nl = s_nlong;")
+    w("#pragma unroll 1")
+    w.open("for (int k = wv; k < nl; k += %d)" % WAVES)
+    w("const int i = s_long[k];")
+    w("const tg_i64 rs = s_ptr[i], re = s_ptr[i + 1];")
+    w("const int st = (int)((rs > p0 ? rs : p0) - p0), en = (int)(re - p0);")
+    w("double acc = 0.0;")
+    w("#pragma unroll 1")
+    w("for (int q = st + l; q < en; q += 64) acc += s_prod[q];")
+    w("acc = tg_segsum<64>(acc);")
+    w.open("if (l == 0 && b0 + i < row_end)")
+    store("acc", "b0 + i")
+    w.close()
+    w.close()
+    w("__syncthreads();  // every wave has read s_nlong, s_long and s_ptr")
+    w("if (threadIdx.x == 0) s_nlong = 0;")
+    w.close()
+
+
 def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeometry,
                        out_name: str, pre: Optional[_W] = None,
                        scratch_arg: bool = False) -> None:
@@ -1203,6 +1452,11 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     each window sums its piece with the whole workgroup and the piece that
     finishes last adds the pieces up in window order (``_merge_decls``).
     """
+    if low.tiled and low.balance == "stream":
+        if pre is None:
+            raise ValueError("stream ranges need file-scope declarations")
+        _hip_stream_reduce(w, plan, low, bound, geo, out_name, pre, scratch_arg)
+        return
     B, TPR = geo.block, max(1, low.threads_per_row)
     U = max(1, low.unroll)
     SLOTS = B // TPR
@@ -2022,6 +2276,13 @@ def _check_hip_dtype(config: Config) -> None:
                          % (config.dtype, config.dtype))
 
 
+def _grid_text(geo: LaunchGeometry) -> str:
+    if geo.stream:
+        return "ceil(nnz / %d) (1 without nonzeros; 0 without rows)" % geo.nnz_chunk
+    return "ceil(%s / %d)%s" % (geo.rows_symbol, geo.rows_per_block,
+                                " + ceil(nnz / %d)" % geo.nnz_chunk if geo.nnz_chunk else "")
+
+
 def emit_hip(kernel: Kernel, config: Config, scratch_arg: bool = False) -> str:
     """Device translation unit of a lowered kernel (hipRTC input).
 
@@ -2041,10 +2302,8 @@ def emit_hip(kernel: Kernel, config: Config, scratch_arg: bool = False) -> str:
     _sig, args, _info = abi_of(kernel)
     geo = launch_geometry(plan, low)
     extra = ["target      : %s (wave%d)" % (HIP_ARCH, WAVE),
-             "launch      : grid = ceil(%s / %d)%s, block = %d, lds = %d B"
-             % (geo.rows_symbol, geo.rows_per_block,
-                " + ceil(nnz / %d)" % geo.nnz_chunk if geo.nnz_chunk else "",
-                geo.block, geo.lds_bytes)]
+             "launch      : grid = %s, block = %d, lds = %d B"
+             % (_grid_text(geo), geo.block, geo.lds_bytes)]
     return "\n".join([_header(kernel, config, "hip", low, extra), _HIP_PRELUDE.strip(), "",
                       _hip_kernel_text(kernel, config, plan, low, args, geo, scratch_arg), ""])
 
@@ -2083,7 +2342,7 @@ def emit_hip_host(kernel: Kernel, config: Config) -> str:
     nnz = "nnz" if "nnz" in dims else "0"
     params = ", ".join("%s %s" % a for a in args)
     text = """/* TileGen HIP launcher for %(sym)s -- generated, DO NOT EDIT.
- * schedule %(sched)s; grid = ceil(%(rows)s / %(rpb)d)%(extra_grid)s, block = %(block)d, lds = %(lds)d B */
+ * schedule %(sched)s; grid = %(grid_text)s, block = %(block)d, lds = %(lds)d B */
 #include <stdint.h>
 #include <string.h>
 #include "tgrt.h"
@@ -2108,7 +2367,7 @@ int tgv_geometry(int64_t M, int64_t N, int64_t K, int64_t nnz,
                  int64_t* grid, int32_t* block, int32_t* lds) {
   (void)N; (void)K; (void)nnz;
   const int64_t rows = %(rows_expr)s;
-  *grid = rows > 0 ? (rows + %(rpb)d - 1) / %(rpb)d : 0;%(extra)s
+  *grid = %(grid_expr)s;%(extra)s
   *block = %(block)d;
   *lds = %(lds)d;
   return 0;
@@ -2139,7 +2398,11 @@ int tgv_launch_async(void* stream, %(params)s) {
         "rows_expr": rows if rows in dims else "M", "params": params,
         "pack": "\n".join(pack), "nargs": len(args), "names": ", ".join(names),
         "sig": sig, "M": "M" if "M" in dims else "0", "N": ndim, "K": kdim, "nnz": nnz,
-        "extra_grid": " + ceil(nnz / %d)" % geo.nnz_chunk if geo.nnz_chunk else "",
+        "grid_text": _grid_text(geo),
+        "grid_expr": ("rows > 0 ? (nnz > 0 ? (nnz + %d - 1) / %d : 1) : 0"
+                      % (geo.nnz_chunk, geo.nnz_chunk) if geo.stream else
+                      "rows > 0 ? (rows + %d - 1) / %d : 0" % (geo.rows_per_block,
+                                                             geo.rows_per_block)),
         "launch": ("\n  /* row pieces are combined through this module's scratch, which one launch"
                    "\n     at a time may use: order after its previous launch on any stream */"
                    "\n  return tg_launch_ordered(tg_code, fn, grid, block, lds, a, n, stream, 0);"
@@ -2147,7 +2410,7 @@ int tgv_launch_async(void* stream, %(params)s) {
                    "\n  return tg_launch(fn, grid, block, lds, a, n, stream, 0);"),
         "extra": ("\n  /* long-row workgroups of hybrid tiles, ahead of the row tiles */"
                   "\n  if (*grid > 0 && nnz > 0) *grid += (nnz + %d - 1) / %d;"
-                  % (geo.nnz_chunk, geo.nnz_chunk)) if geo.nnz_chunk else "",
+                  % (geo.nnz_chunk, geo.nnz_chunk)) if geo.nnz_chunk and not geo.stream else "",
     }
     return text
 

@@ -215,8 +215,10 @@ class Tile(Transform):
     size: int = 0
     #: what a tile holds: ``rows`` (``size`` consecutive rows), ``nnz`` (an equal
     #: share of rows plus nonzeros, about ``size`` rows' worth: merge-path windows)
-    #: or ``hybrid`` (``size`` rows, rows past a length threshold left to
-    #: workgroups that each take an equal range of nonzeros)
+    #: ``hybrid`` (``size`` rows, rows past a length threshold left to
+    #: workgroups that each take an equal range of nonzeros) or ``stream`` (an
+    #: equal range of nonzeros per workgroup and the rows that end in it; ``size``
+    #: is not used)
     by: str = "rows"
     kind: ClassVar[str] = "tile"
 
@@ -461,8 +463,8 @@ def _check_transform(t: Transform, known: set) -> None:
                              % (t.kind, ix.name))
     if isinstance(t, Tile) and t.size <= 0:
         raise ValueError("transform %r factor/size must be > 0" % t.kind)
-    if isinstance(t, Tile) and t.by not in ("rows", "nnz", "hybrid"):
-        raise ValueError("tile 'by' must be 'rows', 'nnz' or 'hybrid', got %r" % t.by)
+    if isinstance(t, Tile) and t.by not in ("rows", "nnz", "hybrid", "stream"):
+        raise ValueError("tile 'by' must be 'rows', 'nnz', 'hybrid' or 'stream', got %r" % t.by)
     if isinstance(t, Split) and t.factor <= 0:
         raise ValueError("transform %r factor/size must be > 0" % t.kind)
     if isinstance(t, Unroll) and t.factor <= 0:

@@ -186,6 +186,14 @@ def tiling(kernel: Kernel) -> Kernel:
              "for nonzero range: long rows' pieces; for %s_o step %d: short %s_i: ..."
              % (outer.name, size, outer.name))
         return kernel
+    if balance == "stream":
+        _log(kernel, "tiling",
+             "split '%s' by nonzeros: each workgroup takes an equal range of nonzeros and "
+             "sums the rows that end in it; rows cut at range edges are shared by the ranges "
+             "they span" % outer.name,
+             "for %s in 0..extent" % outer.name,
+             "for nonzero range: products; for %s ending in the range: sum" % outer.name)
+        return kernel
     if balance == "nnz":
         _log(kernel, "tiling",
              "split '%s' into windows of equal rows-plus-nonzeros (merge path), one per %d "

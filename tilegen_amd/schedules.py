@@ -20,16 +20,19 @@ TUNED: Dict[str, Config] = {
     "c1": Config(tile_size=16, threads_per_row=8, unroll=2, vector_width=1, block_size=128),
     # 7 nonzeros per row: 4 lanes x 2
     "c2": Config(tile_size=128, threads_per_row=4, unroll=2, vector_width=1, block_size=256),
-    # skewed rows, hybrid tiles: rows longer than half of a 2 x B x U nonzero range
+    # c3a (power-law rows, half of them one nonzero long): stream ranges of 2048
+    # nonzeros (512 lanes x 4), rows summed from LDS by 4-lane groups; 11.9-12.1 us
+    # against 13.6-14.1 for the best hybrid tiles (T64/TPR4/U4/B256) and 17.4 for
+    # row tiles alone, three interleaved bench repeats on one box.
+    # c3b: hybrid tiles, rows longer than half of a 2 x B x U nonzero range
     # summed by long-row workgroups over equal ranges, the rest in row tiles.
-    # c3a: ranges of 2048 (rows over 1024), the rest on 4-lane groups in tiles of
-    # 64 rows (13.5 us against 17.4 with row tiles alone).  c3b: ranges of 2048,
-    # so each 2000-nonzero row has one or two pieces and combines in one atomic
-    # round trip, the rest in tiles of 128 rows on 4-lane groups (6.8 us, against
-    # 7.4 for ranges of 1024 and 10.6 for the best row tiles, T32/TPR32/U2/B1024;
-    # five interleaved repeats on one box)
-    "c3a": Config(tile_size=64, threads_per_row=4, unroll=4, vector_width=1, block_size=256,
-                  balance="hybrid"),
+    # Ranges of 2048, so each 2000-nonzero row has one or two pieces and combines
+    # in one atomic round trip, the rest in tiles of 128 rows on 4-lane groups (6.8
+    # us, against 7.4 for ranges of 1024 and 10.6 for the best row tiles,
+    # T32/TPR32/U2/B1024; five interleaved repeats on one box; the best stream
+    # schedule ties it)
+    "c3a": Config(tile_size=128, threads_per_row=4, unroll=4, vector_width=1, block_size=512,
+                  balance="stream"),
     "c3b": Config(tile_size=128, threads_per_row=4, unroll=2, vector_width=1, block_size=512,
                   balance="hybrid"),
     # K = 64: 8 lanes x 2 columns x 4 passes per row, 2 nonzeros' B rows in flight
@@ -104,6 +107,20 @@ MERGE_TEST_SCHEDULES: List[Config] = [
 # ranges of 2 x block x unroll): ranges of 128 to 4096 nonzeros.
 HYBRID_TEST_SCHEDULES: List[Config] = [
     Config(**{**c.to_dict(), "balance": "hybrid"}) for c in MERGE_TEST_SCHEDULES]
+
+
+# The same for stream ranges (an equal range of block x unroll nonzeros per
+# workgroup, rows summed from LDS): one wave (both row searches in one wave) and
+# sixteen, ranges of 64 to 8192 nonzeros, odd and even unroll, every lane-group
+# width tier.  The tile size is not used by this form.
+STREAM_TEST_SCHEDULES: List[Config] = [
+    Config(tile_size=64, threads_per_row=4, unroll=2, block_size=256, balance="stream"),
+    Config(tile_size=64, threads_per_row=1, unroll=1, block_size=64, balance="stream"),
+    Config(tile_size=16, threads_per_row=64, unroll=3, block_size=1024, balance="stream"),
+    Config(tile_size=128, threads_per_row=8, unroll=8, block_size=1024, balance="stream"),
+    Config(tile_size=8, threads_per_row=16, unroll=4, block_size=128, balance="stream"),
+    Config(tile_size=256, threads_per_row=2, unroll=1, block_size=512, balance="stream"),
+]
 
 
 def schedule_id(c: Config) -> str:

@@ -5,9 +5,10 @@ backend: the five standard kernels x three schedules (the reference's own
 list, ``verify_all.py:27-31``) x the six corpus classes, plus one variant with
 ``inject_bug=True`` per class, each through ``verify()`` against float64
 SciPy.  On the HIP backend the SpMV-shaped kernels (spmv, fused_spmv_axpy)
-also run in the two load-balanced forms this build adds (``Config.balance``
-"nnz" for merge-path windows and "hybrid" for row tiles plus long-row
-workgroups), counted apart from the reference's triples.  The result file has
+also run in the three load-balanced forms this build adds (``Config.balance``
+"nnz" for merge-path windows, "hybrid" for row tiles plus long-row workgroups
+and "stream" for equal nonzero ranges), counted apart from the reference's
+triples.  The result file has
 the reference's ``results/correctness.json``
 layout (``summary`` + per-triple ``results``), with the normwise errors and
 the indptr/indices byte check of this build added to each record.
@@ -40,14 +41,15 @@ CONFIGS = [
     Config(tile_size=128, threads_per_row=8, unroll=2, vector_width=2, block_size=512),
 ]
 BUG_CONFIG = Config(tile_size=32, threads_per_row=1, unroll=1, inject_bug=True)
-# HIP only: merge-path windows and hybrid tiles of the SpMV-shaped kernels
+# HIP only: merge-path windows, hybrid tiles and stream ranges of the SpMV-shaped
+# kernels
 BALANCE_KERNELS = ("spmv", "fused_spmv_axpy")
 BALANCE_CONFIGS = [
     Config(tile_size=64, threads_per_row=4, unroll=4, vector_width=1, block_size=256,
-           balance=b) for b in ("nnz", "hybrid")
+           balance=b) for b in ("nnz", "hybrid", "stream")
 ] + [
     Config(tile_size=16, threads_per_row=8, unroll=2, vector_width=1, block_size=128,
-           balance=b) for b in ("nnz", "hybrid")
+           balance=b) for b in ("nnz", "hybrid", "stream")
 ]
 
 
