@@ -5,8 +5,8 @@
  * No counterpart in the reference.  It is for callers that cannot allocate
  * device memory: code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc.  Same arguments and result as launch_spmv
- * (tilegen_launch.h) at the tuned hybrid-tile schedule (row tiles plus
- * long-row workgroups over equal nonzero ranges), plus a stream:
+ * (tilegen_launch.h) at the hybrid-tile schedule T128/TPR4/U2/B512 (row tiles
+ * plus long-row workgroups over equal nonzero ranges), plus a stream:
  *
  *   - y[i] = sum_p data[p] * x[indices[p]] over row i; every pointer is a
  *     device pointer the caller allocated; indptr/indices are never written;

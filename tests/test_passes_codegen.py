@@ -440,11 +440,11 @@ def test_scratch_argument_form_of_scratch_modules():
 
 
 def test_noalloc_kernel_source_geometry():
-    from tilegen_amd.build import NOALLOC_CASE, noalloc_kernel_source
+    from tilegen_amd.build import noalloc_kernel_source
     from tilegen_amd.codegen import MERGE_CAP, hybrid_chunk
-    from tilegen_amd.schedules import TUNED
+    from tilegen_amd.schedules import NOALLOC_SCHEDULE
     src = noalloc_kernel_source()
-    cfg = TUNED[NOALLOC_CASE]
+    cfg = NOALLOC_SCHEDULE
     chunk = 2 * cfg.block_size * cfg.unroll
     assert "#define TG_NA_CHUNK %d " % chunk in src
     assert "#define TG_NA_SLOTS %d " % (2 * MERGE_CAP) in src

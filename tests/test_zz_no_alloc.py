@@ -18,9 +18,8 @@ import pytest
 import oracle
 from tests.util import rel_2, rel_inf
 from tilegen_amd import runtime as rt
-from tilegen_amd.build import NOALLOC_CASE
 from tilegen_amd.matrices import baseline_operands, make_baseline
-from tilegen_amd.schedules import TUNED
+from tilegen_amd.schedules import NOALLOC_SCHEDULE
 from tilegen_amd.variant import Variant
 
 pytestmark = pytest.mark.gpu
@@ -37,7 +36,7 @@ def _noalloc(L, bufs, M, N, nnz):
 
 def test_noalloc_matches_launch_spmv_on_two_calls(hip_ready):
     L = rt.noalloc_lib()
-    v = Variant("spmv", TUNED[NOALLOC_CASE])
+    v = Variant("spmv", NOALLOC_SCHEDULE)
     mats = [("c3a full", make_baseline("c3a")), ("c3b x0.3", make_baseline("c3b", scale=0.3))]
     assert mats[1][1].nnz < mats[0][1].nnz and mats[1][1].shape[0] < mats[0][1].shape[0]
     for label, A in mats:

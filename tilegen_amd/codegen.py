@@ -1345,7 +1345,7 @@ def _hip_stream_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w.open("if (el < %d)" % MERGE_CAP)
     w("const int en = (int)(ra_e - p0);")
     w("double t = 0.0;")
-    w("#pragma unroll 1")
+    w("#pragma unroll 4")
     w("for (int q = l; q < en; q += 64) t += s_prod[q];")
     w("t = tg_segsum<64>(t);")
     w("double tot = t;")
@@ -1360,7 +1360,7 @@ def _hip_stream_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w.open("if (el < %d)" % MERGE_CAP)
     w("const int st = (int)((rb_s > p0 ? rb_s : p0) - p0);")
     w("double t = 0.0;")
-    w("#pragma unroll 1")
+    w("#pragma unroll 4")
     w("for (int q = st + l; q < cnt; q += 64) t += s_prod[q];")
     w("t = tg_segsum<64>(t);")
     w("double tot = t;")
@@ -1399,7 +1399,7 @@ def _hip_stream_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w("const bool own = mine && en - st <= 64;")
     w("double acc = 0.0;")
     w.open("if (own)")
-    w("#pragma unroll 1")
+    w("#pragma unroll 4")
     w("for (int q = st + lane; q < en; q += %d) acc += s_prod[q];" % TPR)
     w.close()
     w("if (mine && !own && lane == 0) s_long[atomicAdd(&s_nlong, 1)] = i;")
@@ -1417,7 +1417,7 @@ def _hip_stream_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w("const tg_i64 rs = s_ptr[i], re = s_ptr[i + 1];")
     w("const int st = (int)((rs > p0 ? rs : p0) - p0), en = (int)(re - p0);")
     w("double acc = 0.0;")
-    w("#pragma unroll 1")
+    w("#pragma unroll 4")
     w("for (int q = st + l; q < en; q += 64) acc += s_prod[q];")
     w("acc = tg_segsum<64>(acc);")
     w.open("if (l == 0 && b0 + i < row_end)")

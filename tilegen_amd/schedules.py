@@ -20,21 +20,19 @@ TUNED: Dict[str, Config] = {
     "c1": Config(tile_size=16, threads_per_row=8, unroll=2, vector_width=1, block_size=128),
     # 7 nonzeros per row: 4 lanes x 2
     "c2": Config(tile_size=128, threads_per_row=4, unroll=2, vector_width=1, block_size=256),
-    # c3a (power-law rows, half of them one nonzero long): stream ranges of 2048
-    # nonzeros (512 lanes x 4), rows summed from LDS by 4-lane groups; 11.9-12.1 us
-    # against 13.6-14.1 for the best hybrid tiles (T64/TPR4/U4/B256) and 17.4 for
-    # row tiles alone, three interleaved bench repeats on one box.
-    # c3b: hybrid tiles, rows longer than half of a 2 x B x U nonzero range
-    # summed by long-row workgroups over equal ranges, the rest in row tiles.
-    # Ranges of 2048, so each 2000-nonzero row has one or two pieces and combines
-    # in one atomic round trip, the rest in tiles of 128 rows on 4-lane groups (6.8
-    # us, against 7.4 for ranges of 1024 and 10.6 for the best row tiles,
-    # T32/TPR32/U2/B1024; five interleaved repeats on one box; the best stream
-    # schedule ties it)
-    "c3a": Config(tile_size=128, threads_per_row=4, unroll=4, vector_width=1, block_size=512,
+    # skewed rows, stream ranges: every workgroup takes an equal range of B x U
+    # nonzeros and sums, from LDS, the rows that end in it.
+    # c3a (power-law rows, half of them one nonzero long): ranges of 4096 (1024
+    # lanes x 4), rows summed by 4-lane groups; 11.3-11.8 us against 12.2 for ranges
+    # of 2048, 13.6-14.1 for the best hybrid tiles (T64/TPR4/U4/B256) and 17.4 for
+    # row tiles alone (interleaved bench repeats on one box).
+    # c3b (1% of rows 2000 long, the rest 4): ranges of 2048 (512 lanes x 4), one
+    # lane per short row; 6.9-7.1 us against 7.4-7.7 for the best hybrid tiles
+    # (T128/TPR4/U2/B512) and 10.6 for the best row tiles (T32/TPR32/U2/B1024)
+    "c3a": Config(tile_size=256, threads_per_row=4, unroll=4, vector_width=1, block_size=1024,
                   balance="stream"),
-    "c3b": Config(tile_size=128, threads_per_row=4, unroll=2, vector_width=1, block_size=512,
-                  balance="hybrid"),
+    "c3b": Config(tile_size=512, threads_per_row=1, unroll=4, vector_width=1, block_size=512,
+                  balance="stream"),
     # K = 64: 8 lanes x 2 columns x 4 passes per row, 2 nonzeros' B rows in flight
     # (fastest of all 882 legal SpMM schedules in a verified sweep on c4; 102.1 us
     # against 103.8 for 16 lanes x 2 passes in three interleaved repeats)
@@ -47,6 +45,12 @@ TUNED: Dict[str, Config] = {
     # chunked-path schedules in a verified sweep on that matrix
     "c5x25": Config(tile_size=16, threads_per_row=8, unroll=4, vector_width=2, block_size=128),
 }
+
+# The schedule of launch_spmv_noalloc (include/tilegen_noalloc.h): hybrid tiles,
+# row tiles of 128 rows on 4-lane groups plus long-row workgroups over ranges of
+# 2048 nonzeros (c3b's tuned schedule before stream ranges took it over).
+NOALLOC_SCHEDULE = Config(tile_size=128, threads_per_row=4, unroll=2, vector_width=1,
+                          block_size=512, balance="hybrid")
 
 # CPU-tuned OpenMP schedules per BASELINE case (``python -m tilegen_amd.cpu_tuned``:
 # random search, budget 40, seed 0, on the GPU box's host); bench.py times them
