@@ -97,6 +97,19 @@ def test_injected_bug_is_caught(kernel, hip_ready, tmp_path):
     assert r.max_abs_err > r.tolerance
 
 
+@pytest.mark.parametrize("balance", ["nnz", "hybrid", "stream"])
+@pytest.mark.parametrize("kernel", ["spmv", "fused_spmv_axpy"])
+def test_injected_bug_is_caught_in_balanced_forms(kernel, balance, hip_ready, tmp_path):
+    """The reference's bug injection (the last row is never written) in the
+    merge-path, hybrid and stream forms: verify() must fail it."""
+    cfg = Config(tile_size=32, threads_per_row=4, unroll=2, vector_width=1, block_size=256,
+                 inject_bug=True, balance=balance)
+    r = verify(kernel, cfg, mixed_257(), backend="hip", workdir=str(tmp_path), K=8)
+    assert r.executed and "compile error" not in r.message, r.message
+    assert not r.ok, "%s %s: injected bug not detected" % (kernel, balance)
+    assert r.max_abs_err > r.tolerance
+
+
 @pytest.mark.parametrize("kernel", TEST_KERNELS)
 @pytest.mark.parametrize("cfg", ODD_BLOCK_SCHEDULES,
                          ids=[schedule_id(c) for c in ODD_BLOCK_SCHEDULES])
