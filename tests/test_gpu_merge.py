@@ -207,8 +207,8 @@ def _device_set(A, ops, out_len):
 
 @pytest.mark.parametrize("case_id", ["c3a", "c3b"])
 def test_scratch_variant_on_two_streams(case_id, hip_ready):
-    """The tuned skewed-row variants (stream ranges on c3a, hybrid tiles on c3b)
-    combine row pieces through one module scratch per device.  Launches on two streams, enqueued back to back with no
+    """The tuned skewed-row variants (stream ranges on c3a and c3b) combine row
+    pieces through one module scratch per device.  Launches on two streams, enqueued back to back with no
     host synchronization in between (and two more on the null stream), are
     ordered by the launcher, so every output equals a serial launch's bits."""
     from tilegen_amd import runtime as rt
