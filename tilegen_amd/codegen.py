@@ -1230,7 +1230,9 @@ def _hip_stream_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
 
     1. Every lane loads its U nonzeros (128-bit (index, value) pairs, coalesced
        over the workgroup), then waves 0 and 1 find ra and rb with
-       ``tg_mp_row`` while those loads are in flight.  The operands are
+       ``tg_st_row`` (the merge path's row search with a first round spread
+       over 2048 rows either side of the proportional guess) while those
+       loads are in flight.  The operands are
        gathered and the products staged in LDS.  Nothing here depends on row
        lengths, so the matrix streams at full width however skewed it is.
     2. After one barrier, the row pieces cut at range edges are committed
@@ -1272,6 +1274,33 @@ def _hip_stream_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
             _cexpr(plan.final_expr, env), out_name, _offset(plan.out_tensor, plan.out.indices, env)))
 
     _merge_decls(pre, scratch_arg)
+    pre(r"""// The row holding nonzero position P, 0 <= P < X = indptr[R], with its bounds in *rs
+// and *re: tg_mp_row's contract and later rounds, with a first round for skewed rows.
+// It probes every 64th row across 2048 rows either side of the proportional guess, so
+// a row that close is found in two rounds (the second probes its bracket row by row);
+// the rows of a power-law or dense-row matrix lie within that distance of the guess.
+__device__ tg_i64 tg_st_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 P, tg_i64 X,
+                            tg_i64* rs, tg_i64* re) {
+  const int l = threadIdx.x & 63;
+  tg_i64 q = (tg_i64)((double)P * ((double)R / (double)X)) + (tg_i64)(l - 32) * 64;
+  tg_i64 lo = 0, hi = R, vlo = 0, vhi = X;   // indptr[0] = 0, indptr[R] = X
+  #pragma unroll 1
+  for (;;) {
+    q = q < lo ? lo : (q > hi ? hi : q);
+    const tg_i64 v = indptr[q];
+    const unsigned long long m = __ballot(v > P);
+    const int f = m ? (int)__builtin_ctzll(m) : 64;   // first lane past P
+    if (f < 64) { hi = tg_lane_read(q, f); vhi = tg_lane_read(v, f); }
+    if (f > 0) { lo = tg_lane_read(q, f - 1); vlo = tg_lane_read(v, f - 1); }
+    if (hi - lo <= 1) {
+      *rs = vlo;
+      *re = vhi;
+      return lo;
+    }
+    q = lo + 1 + (tg_i64)l * ((hi - lo + 61) / 63);   // rows strictly inside the bracket
+  }
+}
+""")
     if not scratch_arg:
         w("unsigned long long* const tg_part = tg_mp_part;")
     w("const tg_i64 row_end = %s;  // rows written" % bound)
@@ -1324,7 +1353,7 @@ def _hip_stream_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w("const tg_i64 P = k == 0 ? p0 : p1;")
     w("tg_i64 r = n_rows, rs = nnz, re = nnz;")
     w("if (k == 0 && e == 0) { r = 0; rs = 0; re = 0; }")
-    w("else if (P < nnz) r = tg_mp_row(indptr, n_rows, P, nnz, &rs, &re);")
+    w("else if (P < nnz) r = tg_st_row(indptr, n_rows, P, nnz, &rs, &re);")
     w("if (l == 0) { s_b[3 * k] = r; s_b[3 * k + 1] = rs; s_b[3 * k + 2] = re; }")
     w.close()
     w("// the operands (positions past the range gather nothing) and the products, in LDS")
