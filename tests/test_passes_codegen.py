@@ -418,16 +418,18 @@ def test_scratch_modules_launch_in_order(balance, ordered):
         assert ("tg_mp_part" in emit_hip(k, cfg)) == ordered
 
 
-def test_scratch_argument_form_of_scratch_modules():
+@pytest.mark.parametrize("balance", ["nnz", "hybrid", "stream"])
+def test_scratch_argument_form_of_scratch_modules(balance):
     """scratch_arg: the same kernel with its slots as a last parameter and no
     module array; refused for variants that combine nothing."""
-    cfg = Config(tile_size=64, threads_per_row=4, unroll=4, block_size=256, balance="hybrid")
+    cfg = Config(tile_size=64, threads_per_row=4, unroll=4, block_size=256, balance=balance)
     k = _run(standard_kernels()["spmv"], cfg, "hip")
     mod, arg = emit_hip(k, cfg), emit_hip(k, cfg, scratch_arg=True)
     assert "__device__ unsigned long long tg_mp_part[" in mod
     assert "tg_mp_part" not in arg
     assert "unsigned long long* __restrict__ tg_part)" in arg
     assert "unsigned long long* const tg_part = tg_mp_part;" in mod
+    assert "tg_mp_commit(tg_part," in arg
 
     def code(t):  # the lines that do not name where the slots come from
         t = t.replace(", unsigned long long* __restrict__ tg_part)", ")")
