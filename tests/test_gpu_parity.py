@@ -298,6 +298,12 @@ OFFSET_CASES = [
     ("sddmm", Config(tile_size=16, threads_per_row=8, unroll=4, vector_width=2, block_size=128)),
     ("sddmm", Config(tile_size=8, threads_per_row=16, unroll=2, vector_width=2, block_size=128)),
     ("axpy", Config(tile_size=64, threads_per_row=1, unroll=4, vector_width=2, block_size=256)),
+    # the balanced forms: pair loads of ranges and pieces, commits of cut rows
+    ("spmv", Config(tile_size=64, threads_per_row=4, unroll=4, block_size=256, balance="hybrid")),
+    ("spmv", Config(tile_size=128, threads_per_row=4, unroll=4, block_size=512, balance="stream")),
+    ("spmv", Config(tile_size=64, threads_per_row=1, unroll=1, block_size=64, balance="stream")),
+    ("fused_spmv_axpy", Config(tile_size=256, threads_per_row=4, unroll=4, block_size=1024,
+                               balance="stream")),
 ]
 
 
