@@ -404,9 +404,10 @@ def test_hip_verify_reports_non_f64_as_compile_error(tmp_path):
     assert not r.ok and "float64 only" in r.message
 
 
-@pytest.mark.parametrize("balance,ordered", [("rows", False), ("nnz", True), ("hybrid", True)])
+@pytest.mark.parametrize("balance,ordered", [("rows", False), ("nnz", True), ("hybrid", True),
+                                             ("stream", True)])
 def test_scratch_modules_launch_in_order(balance, ordered):
-    """Merge-path and hybrid modules share one scratch per device: their
+    """Merge-path, hybrid and stream modules share one scratch per device: their
     launchers order each launch after the previous one on any stream."""
     cfg = Config(tile_size=64, threads_per_row=4, unroll=4, block_size=256, balance=balance)
     for name in ("spmv", "fused_spmv_axpy"):
@@ -453,3 +454,25 @@ def test_noalloc_kernel_source_geometry():
     assert "#define TG_NA_MAX_NNZ %dLL" % (MERGE_CAP * chunk) in src
     assert "#define TG_NA_BLOCK %d" % cfg.block_size in src
     assert "__device__ unsigned long long tg_mp_part[" not in src
+
+
+def test_stream_tile_through_passes_and_ir():
+    """balance="stream" lowers to Tile(i, T, by=stream): the tiling pass logs the
+    nonzero split, the IR round-trips it, and the schedule's name and hash carry
+    it without touching a reference schedule's."""
+    from tilegen_amd.ir import Kernel, Tile
+    cfg = Config(tile_size=128, threads_per_row=4, unroll=4, block_size=512, balance="stream")
+    k = _run(standard_kernels()["spmv"], cfg, "hip")
+    tiles = [t for t in k.schedule if isinstance(t, Tile)]
+    assert len(tiles) == 1 and tiles[0].by == "stream"
+    assert "by=stream" in k.pretty()
+    log = [r for r in k.pass_log if r["pass"] == "tiling"][0]["action"]
+    assert "equal range of nonzeros" in log
+    again = Kernel.from_dict(k.to_dict())
+    assert [t for t in again.schedule if isinstance(t, Tile)][0].by == "stream"
+    assert cfg.short().endswith("/stream") and cfg.to_dict()["balance"] == "stream"
+    plain = Config(tile_size=128, threads_per_row=4, unroll=4, block_size=512)
+    assert cfg.hash() != plain.hash() and "balance" not in plain.to_dict()
+    gen = generate(standard_kernels()["spmv"], cfg, "hip", write=False)
+    assert gen.geometry.stream and gen.geometry.nnz_chunk == 2048
+    assert "grid = ceil(nnz / 2048)" in gen.source
