@@ -2315,15 +2315,15 @@ def _grid_text(geo: LaunchGeometry) -> str:
 def emit_hip(kernel: Kernel, config: Config, scratch_arg: bool = False) -> str:
     """Device translation unit of a lowered kernel (hipRTC input).
 
-    ``scratch_arg`` (merge-path and hybrid variants only): the kernel takes the
+    ``scratch_arg`` (merge-path, hybrid and stream variants only): the kernel takes the
     slots it combines row pieces through as a last parameter,
     ``unsigned long long* tg_part`` (2 * MERGE_CAP of them, all zero between
     launches), instead of declaring them as module scratch."""
     _check_hip_dtype(config)
     plan, low = _plan(kernel), _lowering(kernel)
     if scratch_arg and not module_scratch(plan, low):
-        raise ValueError("scratch_arg applies to merge-path and hybrid variants only; %s "
-                         "combines nothing across workgroups" % config.short())
+        raise ValueError("scratch_arg applies to merge-path, hybrid and stream variants "
+                         "only; %s combines nothing across workgroups" % config.short())
     if config.balance != "rows" and config.tile_size <= 1:
         raise ValueError("balance '%s' needs a tile (tile_size > 1); %s is untiled"
                          % (config.balance, config.short()))

@@ -121,7 +121,7 @@ def render_table(payload: Dict[str, Any]) -> str:
             "yes" if r["inject_bug"] else ""))
     head = [
         "# Differential test, %s backend" % s["backend"], "",
-        "normal triples passed: %d / %d (of which merge-path and hybrid forms: %d / %d); "
+        "normal triples passed: %d / %d (of which load-balanced forms: %d / %d); "
         "injected bugs caught: %d / %d; max abs err %.3e; "
         "max normwise relative error %.3e (inf-norm), %.3e (2-norm); indptr/indices intact: %s."
         % (s["normal_passed"], s["normal_triples"], s.get("balance_passed", 0),
