@@ -22,7 +22,7 @@ import pytest
 
 from tilegen_amd import runtime as rt
 from tilegen_amd.codegen import Config
-from tilegen_amd.schedules import TEST_SCHEDULES, TUNED
+from tilegen_amd.schedules import MERGE_TEST_SCHEDULES, NOALLOC_SCHEDULE, TEST_SCHEDULES, TUNED
 from tilegen_amd.variant import Variant
 from tilegen_amd.verify import hiprtc_options
 
@@ -118,7 +118,15 @@ def _structure_unchanged(bufs, ip, nnz):
         assert np.array_equal(got, np.arange(start, start + 4096, dtype=np.int64) % N)
 
 
-@pytest.mark.parametrize("cfg", [TUNED["c1"], TEST_SCHEDULES[0]], ids=lambda c: c.short())
+# row tiles, the tuned stream ranges (4096 and 2048 nonzeros), hybrid tiles and
+# merge-path windows; at this size every long row from about p = 2^28 on has
+# pieces past the 65536 ranges with scratch slots, so the stream and hybrid forms
+# also sum those rows whole, with the whole workgroup of the range each begins in
+_SPMV_HUGE = [TUNED["c1"], TEST_SCHEDULES[0], TUNED["c3a"], TUNED["c3b"], NOALLOC_SCHEDULE,
+              MERGE_TEST_SCHEDULES[1]]
+
+
+@pytest.mark.parametrize("cfg", _SPMV_HUGE, ids=lambda c: c.short())
 def test_spmv_past_2_31_nonzeros(huge, cfg):
     ip, M, nnz, bufs = huge
     x = (np.arange(N, dtype=np.int64) % 7) - 3
@@ -128,6 +136,7 @@ def test_spmv_past_2_31_nonzeros(huge, cfg):
     by = rt.DeviceBuffer(np.zeros(M))
     try:
         v = Variant("spmv", cfg)
+        print("[huge] spmv %s M=%d nnz=%d" % (cfg.short(), M, nnz), flush=True)
         v.device_call(v.abi_values(None, dict(bufs, x=bx, y=by), {}, M, N, 0, nnz))
         got = by.to_host()
     finally:

@@ -256,10 +256,10 @@ def _kernel(name, cfg):
 
 
 def _stream_scratch_matrix(CH):
-    """About 75000 ranges of CH = 64 nonzeros: a long row near the top (cut into
+    """About 75000 ranges of CH nonzeros: a long row near the top (cut into
     pieces inside the scratch), one straddling the last range with slots, and
     one beginning past it."""
-    rows, max_len, seed = 160_000, 60, 41
+    rows, max_len, seed = 2500 * CH, 60, 41
     lengths = np.random.default_rng(seed).integers(0, max_len + 1, size=rows)
     lengths[10] = 700
     starts = np.concatenate([[0], np.cumsum(lengths)])
@@ -268,16 +268,20 @@ def _stream_scratch_matrix(CH):
                   long_rows=[(10, 700), (edge, 900), (rows - 60, 900)]), edge
 
 
-def test_stream_more_ranges_than_scratch(hip_ready):
+@pytest.mark.parametrize("cfg", [
+    Config(tile_size=64, threads_per_row=1, unroll=1, block_size=64, balance="stream"),
+    Config(tile_size=64, threads_per_row=4, unroll=1, block_size=128, balance="stream"),
+], ids=["one-wave", "two-waves"])
+def test_stream_more_ranges_than_scratch(cfg, hip_ready):
     """More ranges than the 65536 with scratch slots: the long row near the top
     is combined through the scratch; the row straddling the last range with
     slots and the row beginning past it are summed whole, with their own loads,
-    by the range each begins in."""
-    cfg = Config(tile_size=64, threads_per_row=1, unroll=1, block_size=64, balance="stream")
+    by the workgroup of the range each begins in (one wave, then two, whose sums
+    are added in wave order)."""
     CH = Variant("spmv", cfg).gen.geometry.nnz_chunk
     A, edge = _stream_scratch_matrix(CH)
     rows, ip = A.shape[0], A.indptr
-    assert CH == 64 and -(-A.nnz // CH) > cg.MERGE_CAP
+    assert CH == cfg.block_size and -(-A.nnz // CH) > cg.MERGE_CAP
     assert ip[10] // CH < (ip[11] - 1) // CH < cg.MERGE_CAP
     assert ip[edge] // CH < cg.MERGE_CAP <= (ip[edge + 1] - 1) // CH
     assert cg.MERGE_CAP <= ip[rows - 60] // CH < (ip[rows - 59] - 1) // CH

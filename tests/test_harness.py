@@ -84,11 +84,12 @@ def test_hip_backend_device_buffers(kernel, matrix_bin, tmp_path, hip_ready):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("balance", ["nnz", "hybrid"])
+@pytest.mark.parametrize("balance", ["nnz", "hybrid", "stream"])
 def test_hip_harness_balance_modes(balance, matrix_bin, tmp_path, hip_ready):
     """The harness takes its grid from tgv_geometry, which counts the hybrid
-    tiles' range workgroups; with windows and ranges of a few rows, the
-    240-nonzero row is cut into pieces, and the result still matches."""
+    tiles' range workgroups and, for stream ranges, one workgroup per range of
+    64 nonzeros; with windows and ranges of a few rows, the 240-nonzero row is
+    cut into pieces, and the result still matches."""
     so = _lib("spmv", "hip", tmp_path, Config(tile_size=2, threads_per_row=4, unroll=1,
                                               block_size=64, balance=balance))
     r = _run("--kernel", "spmv", "--matrix", matrix_bin, "--lib", so, "--backend", "hip",

@@ -722,7 +722,7 @@ def launch_geometry(plan: Plan, low: Lowering) -> LaunchGeometry:
     rows = low.tile if low.tiled else slots
     if plan.kind == "scalar_reduce" and low.tiled and low.balance == "stream":
         CH, RB = stream_chunk(low), stream_batch(low)
-        lds = 8 * CH + 8 * (RB + 1) + 4 * RB + 8 * 6 + 4
+        lds = 8 * CH + 8 * (RB + 1) + 4 * RB + 8 * 6 + 4 + 8 * max(1, B // WAVE)
         return LaunchGeometry(1, B, lds, plan.row_extent, CH, stream=True)
     lds = 8 * (rows + 1) if (plan.kind == "scalar_reduce" and low.tiled) else 0
     chunk = hybrid_chunk(low) if (plan.kind == "scalar_reduce" and low.tiled
@@ -1239,11 +1239,13 @@ def _hip_stream_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
        first, so that their atomic round trips overlap the row sums: wave 0
        the last piece of row ra when it began in an earlier range, wave 1 this
        range's piece of row rb.  ``tg_mp_commit`` adds the pieces in range
-       order.  A row with a piece in a range past the scratch's MERGE_CAP
-       ranges is summed whole, with its own loads, by the range it begins in.
+       order.
     3. The owned rows' pointers are staged RB at a time, and each row is summed
        from the staged products by a lane group of TPR lanes (DPP); rows over
        64 nonzeros are listed and summed by one wave each.
+    4. A row with a piece in a range past the scratch's MERGE_CAP ranges is
+       summed whole, with its own loads, by the whole workgroup of the range it
+       begins in, the waves' sums added in wave order.
     """
     if not _value_row_free(plan):
         raise ValueError("stream ranges need a per-nonzero value that reads only the sparse "
@@ -1310,6 +1312,7 @@ __device__ tg_i64 tg_st_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 
     w("__shared__ tg_i64 s_b[6];  // the rows holding p0 and p1: row, start, end")
     w("__shared__ int s_long[%d];  // staged rows over 64 nonzeros" % RB)
     w("__shared__ int s_nlong;")
+    w("__shared__ double s_wsum[%d];  // the waves' sums of a row past the scratch" % WAVES)
     w("const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);")
     w("const int l = threadIdx.x & 63;")
     w("const tg_i64 e = blockIdx.x;")
@@ -1397,19 +1400,7 @@ __device__ tg_i64 tg_st_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 
     store("tot", "rb")
     w.close()
     w.close()
-    w.open("else if (ef == e)")
-    w("// a row reaching past the scratch's last range: summed whole by its first range")
-    w("double t = 0.0;")
-    w("#pragma unroll 1")
-    w.open("for (tg_i64 pq = rb_s + l; pq < rb_e; pq += 64)")
-    w("const tg_i64 cq = indices[pq];")
-    w("t += %s;" % _value_with(plan, "data[pq]", gather("cq"), row, "cq"))
-    w.close()
-    w("t = tg_segsum<64>(t);")
-    w.open("if (l == 0 && rb < row_end)")
-    store("t", "rb")
-    w.close()
-    w.close()
+    w("// otherwise, when it begins here, this workgroup sums it whole (below)")
     w.close()
     w("// 3. the owned rows [ra, rb), %d row pointers at a time" % RB)
     w("const int lane = threadIdx.x %% %d;" % TPR)
@@ -1455,6 +1446,27 @@ __device__ tg_i64 tg_st_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 
     w.close()
     w("__syncthreads();  // every wave has read s_nlong, s_long and s_ptr")
     w("if (threadIdx.x == 0) s_nlong = 0;")
+    w.close()
+    w("// 4. row rb, when it begins in this range and reaches past the scratch's last range:")
+    w("// summed whole by the whole workgroup with its own loads, the waves' sums added in")
+    w("// wave order (the condition is the same for every wave)")
+    w.open("if (rb < n_rows && rb_s < p1 && rb_s / %d == e && (rb_e - 1) / %d >= %d)"
+           % (CH, CH, MERGE_CAP))
+    w("double t = 0.0;")
+    w("#pragma unroll 4")
+    w.open("for (tg_i64 pq = rb_s + (tg_i64)threadIdx.x; pq < rb_e; pq += %d)" % B)
+    w("const tg_i64 cq = indices[pq];")
+    w("t += %s;" % _value_with(plan, "data[pq]", gather("cq"), row, "cq"))
+    w.close()
+    w("t = tg_segsum<64>(t);")
+    w("if (l == 0) s_wsum[wv] = t;")
+    w("__syncthreads();")
+    w.open("if (threadIdx.x == 0 && rb < row_end)")
+    w("double tot = 0.0;")
+    w("#pragma unroll")
+    w("for (int v = 0; v < %d; ++v) tot += s_wsum[v];" % WAVES)
+    store("tot", "rb")
+    w.close()
     w.close()
 
 
