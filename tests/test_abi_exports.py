@@ -106,6 +106,24 @@ def test_runtime_error_reporting_without_device():
     assert "null function" in runtime.last_error()
 
 
+@pytest.mark.parametrize("grid,block", [(1 << 22, 1024), ((1 << 32) // 64, 64), (1, 1025),
+                                        (-1, 64), (1, 0)])
+def test_launch_geometry_refused_before_any_device_call(grid, block):
+    """A dispatch's grid is a 32-bit count of work-items, and a workgroup holds
+    at most 1024 lanes: both launch entry points refuse anything else with an
+    error before any HIP call (the function handle here is never called)."""
+    L = runtime.lib()
+    fake = ctypes.c_void_p(0x1000)
+    key = ctypes.c_char_p(b"key")
+    for name, call in (
+            ("tg_launch", lambda: L.tg_launch(fake, grid, block, 0, None, 0, None, 1)),
+            ("tg_launch_ordered",
+             lambda: L.tg_launch_ordered(key, fake, grid, block, 0, None, 0, None, 1))):
+        L.tg_clear_error()
+        assert call() == -1, name
+        assert "invalid geometry" in runtime.last_error(), (name, runtime.last_error())
+
+
 def test_rtc_compile_and_errors():
     code, _ = runtime.rtc_compile('extern "C" __global__ void k(double* a) { a[0] = 1.0; }',
                                   "k.hip", ["--offload-arch=gfx950", "-O3"])

@@ -336,6 +336,9 @@ int tg_launch_ordered(const void* order_key, tg_function fn, int64_t grid, int32
   if (!order_key) return fail(-1, "tg_launch_ordered: null order key");
   if (!fn) return fail(-1, "tg_launch_ordered: null function");
   if (grid == 0) return 0;
+  if (!valid_geometry(grid, block))
+    return fail(-1, "tg_launch_ordered: invalid geometry grid=%lld block=%d", (long long)grid,
+                block);
   int device = 0;
   TG_HIP(hipGetDevice(&device), "hipGetDevice");
   hipStream_t s = static_cast<hipStream_t>(stream);
