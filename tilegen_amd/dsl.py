@@ -63,8 +63,10 @@ class Tensor:
     def shape(self) -> Tuple[Any, ...]:
         return self.decl.shape
 
-    def __repr__(self) -> str:  # pragma: no cover - cosmetic
-        return "Tensor(%s, %s)" % (self.decl.name, self.decl.format.name)
+    def __repr__(self) -> str:
+        d = self.decl
+        return "<%s: %s %s%s>" % (d.name, d.dtype, d.format.name,
+                                  "" if not d.shape else " " + "x".join(map(str, d.shape)))
 
 
 def tensor(name: str, fmt: Format, shape: Sequence[Any] = (), dtype: str = "f64") -> Tensor:
@@ -75,11 +77,15 @@ def tensor(name: str, fmt: Format, shape: Sequence[Any] = (), dtype: str = "f64"
 def sparse_tensor(name: str, fmt: Format, shape: Sequence[Any] = (),
                   dtype: str = "f64") -> Tensor:
     if not fmt.is_sparse():
-        raise ValueError("sparse_tensor requires a compressed format, got %r" % fmt.name)
+        raise ValueError("sparse_tensor(%r): format %s stores every level dense; pass a "
+                         "format with a compressed level such as CSR, or use dense_tensor"
+                         % (name, fmt.name))
     return tensor(name, fmt, shape, dtype)
 
 
 def dense_tensor(name: str, shape: Sequence[Any] = (), dtype: str = "f64") -> Tensor:
+    # orders 0-2 take the IR's named format objects, so the kernels' IR compares and
+    # serialises like the reference's; higher orders get an all-dense format of their own
     order = len(shape)
     fmt = {0: SCALAR, 1: DENSE1, 2: DENSE2}.get(order) or \
         Format("dense%d" % order, ("dense",) * order)
