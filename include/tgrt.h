@@ -124,6 +124,20 @@ int tg_stream_create(void** stream);
 int tg_stream_destroy(void* stream);
 int tg_stream_synchronize(void* stream);
 
+/* ---- HIP graphs ----
+ * tg_graph_begin starts capturing `stream` (not the null stream; thread-local
+ * mode); launches enqueued on it are recorded, not run.  tg_graph_end ends the
+ * capture and instantiates the graph into *exec; tg_graph_launch replays it on
+ * `stream` (sync != 0 waits); tg_graph_destroy frees it.  The generated
+ * launchers' tgv_launch_async and launch_spmv_noalloc may be captured.  A
+ * captured launch of a module with scratch is not ordered against that
+ * module's eager launches: the caller orders replays and eager calls.  No
+ * counterpart in the reference, which has no graph layer. */
+int tg_graph_begin(void* stream);
+int tg_graph_end(void* stream, void** exec);
+int tg_graph_launch(void* exec, void* stream, int sync);
+int tg_graph_destroy(void* exec);
+
 #ifdef __cplusplus
 }
 #endif

@@ -124,6 +124,19 @@ def test_launch_geometry_refused_before_any_device_call(grid, block):
         assert "invalid geometry" in runtime.last_error(), (name, runtime.last_error())
 
 
+def test_graph_entry_points_refuse_null_arguments():
+    """Refused before any HIP call: the null stream cannot be captured, and a
+    null graph is neither launched nor an error to destroy."""
+    L = runtime.lib()
+    for call, text in ((lambda: L.tg_graph_begin(None), "null stream cannot be captured"),
+                       (lambda: L.tg_graph_end(None, None), "null stream"),
+                       (lambda: L.tg_graph_launch(None, None, 1), "null graph")):
+        L.tg_clear_error()
+        assert call() == -1
+        assert text in runtime.last_error()
+    assert L.tg_graph_destroy(None) == 0
+
+
 def test_rtc_compile_and_errors():
     code, _ = runtime.rtc_compile('extern "C" __global__ void k(double* a) { a[0] = 1.0; }',
                                   "k.hip", ["--offload-arch=gfx950", "-O3"])

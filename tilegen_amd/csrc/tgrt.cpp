@@ -493,4 +493,43 @@ int tg_stream_synchronize(void* stream) {
   return 0;
 }
 
+int tg_graph_begin(void* stream) {
+  // the null stream cannot be captured; thread-local mode leaves other threads free
+  if (!stream) return fail(-1, "tg_graph_begin: the null stream cannot be captured");
+  TG_HIP(hipStreamBeginCapture(static_cast<hipStream_t>(stream),
+                               hipStreamCaptureModeThreadLocal),
+         "hipStreamBeginCapture");
+  return 0;
+}
+
+int tg_graph_end(void* stream, void** exec) {
+  if (!stream) return fail(-1, "tg_graph_end: null stream");
+  hipGraph_t graph = nullptr;
+  // the capture is ended even when the caller gave no output, so the stream is usable again
+  TG_HIP(hipStreamEndCapture(static_cast<hipStream_t>(stream), &graph), "hipStreamEndCapture");
+  if (!exec) {
+    if (graph) hipGraphDestroy(graph);
+    return fail(-1, "tg_graph_end: null output");
+  }
+  hipGraphExec_t e = nullptr;
+  const hipError_t err = hipGraphInstantiate(&e, graph, nullptr, nullptr, 0);
+  hipGraphDestroy(graph);
+  if (err != hipSuccess) return hip_fail(err, "hipGraphInstantiate");
+  *exec = e;
+  return 0;
+}
+
+int tg_graph_launch(void* exec, void* stream, int sync) {
+  if (!exec) return fail(-1, "tg_graph_launch: null graph");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  TG_HIP(hipGraphLaunch(static_cast<hipGraphExec_t>(exec), s), "hipGraphLaunch");
+  if (sync) TG_HIP(s ? hipStreamSynchronize(s) : hipDeviceSynchronize(), "synchronize");
+  return 0;
+}
+
+int tg_graph_destroy(void* exec) {
+  if (exec) TG_HIP(hipGraphExecDestroy(static_cast<hipGraphExec_t>(exec)), "hipGraphExecDestroy");
+  return 0;
+}
+
 }  // extern "C"

@@ -19,7 +19,8 @@ import numpy as np
 __all__ = [
     "TileGenHipError", "lib", "lib_path", "include_dir", "check", "device_count",
     "device_info", "rtc_compile", "DeviceBuffer", "launch", "time_launches",
-    "pack_args", "synchronize", "ArgSets", "run_launches",
+    "pack_args", "synchronize", "ArgSets", "run_launches", "stream_create", "stream_destroy",
+    "stream_synchronize", "graph_capture", "graph_launch", "graph_destroy",
 ]
 
 _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
@@ -103,6 +104,10 @@ def _declare(L) -> None:
         "tg_stream_create": (ctypes.c_int, [ctypes.POINTER(_vp)]),
         "tg_stream_destroy": (ctypes.c_int, [_vp]),
         "tg_stream_synchronize": (ctypes.c_int, [_vp]),
+        "tg_graph_begin": (ctypes.c_int, [_vp]),
+        "tg_graph_end": (ctypes.c_int, [_vp, ctypes.POINTER(_vp)]),
+        "tg_graph_launch": (ctypes.c_int, [_vp, _vp, ctypes.c_int]),
+        "tg_graph_destroy": (ctypes.c_int, [_vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -269,6 +274,30 @@ def stream_destroy(stream: int) -> None:
 
 def stream_synchronize(stream: int) -> None:
     check(lib().tg_stream_synchronize(stream), "tg_stream_synchronize")
+
+
+def graph_capture(stream: int, enqueue) -> int:
+    """Capture what ``enqueue()`` launches on ``stream`` (a ``stream_create``
+    handle) into an instantiated HIP graph and return its handle (replay with
+    ``graph_launch``, free with ``graph_destroy``).  The capture is ended even
+    when ``enqueue`` raises."""
+    L = lib()
+    check(L.tg_graph_begin(stream), "tg_graph_begin")
+    exec_ = ctypes.c_void_p()
+    try:
+        enqueue()
+    finally:
+        rc = L.tg_graph_end(stream, ctypes.byref(exec_))
+    check(rc, "tg_graph_end")
+    return int(exec_.value)
+
+
+def graph_launch(exec_: int, stream: int, sync: bool = True) -> None:
+    check(lib().tg_graph_launch(exec_, stream, 1 if sync else 0), "tg_graph_launch")
+
+
+def graph_destroy(exec_: int) -> None:
+    check(lib().tg_graph_destroy(exec_), "tg_graph_destroy")
 
 
 def pack_args(values: Sequence) -> List[int]:
