@@ -3,9 +3,9 @@ point that allocates nothing, against launch_spmv of the same schedule.
 
 Two calls in a row on one device, the second with a smaller matrix, each
 through the C ABI with device pointers and an output pre-filled with NaN; both
-must match launch_spmv's result within the 1e-10 normwise bar (and the C
-oracle), leave indptr/indices untouched, and leave the library's static scratch
-ready for the next call.  Sizes past the scratch's limit and bad arguments are
+must match launch_spmv's result bit for bit (the same kernel source, its slots
+passed in) and the C oracle within the 1e-10 normwise bar, leave indptr/indices
+untouched, and leave the library's static scratch ready for the next call.  Sizes past the scratch's limit and bad arguments are
 refused before anything is launched."""
 
 from __future__ import annotations
@@ -61,6 +61,8 @@ def test_noalloc_matches_launch_spmv_on_two_calls(hip_ready):
                 assert ri <= TOL and r2 <= TOL, "%s vs %s: %g %g" % (label, name, ri, r2)
             print("[gpu] noalloc %s max |diff| vs launch_spmv %.3g" % (
                 label, float(np.abs(got - want).max())), flush=True)
+            # the same kernel source with its slots passed in: the same bits
+            assert np.array_equal(got, want), label
             for k in ("indptr", "indices"):
                 assert bufs[k].to_host().tobytes() == host[k].tobytes(), k
         finally:
