@@ -1656,16 +1656,70 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w("acc[r] = 0.0;")
     w.close()
 
-    w("// first step of every row in flight before any accumulation")
-    w("#pragma unroll")
-    w.open("for (int r = 0; r < %d; ++r)" % R)
-    w("const tg_i64 row = row0 + slot + r * %d;" % SLOTS)
-    w("(void)row;")
-    w("const tg_i64 q = (rs[r] & ~(tg_i64)%d) + (tg_i64)lane * %d;" % (ALIGN - 1, U))
-    w.open("if (q < re[r] && rs[r] < re[r])")
-    step("q", "rs[r]", "re[r]", "acc[r]")
-    w.close()
-    w.close()
+    if R == 1:
+        w("// first step of every row in flight before any accumulation")
+        w("#pragma unroll")
+        w.open("for (int r = 0; r < %d; ++r)" % R)
+        w("const tg_i64 row = row0 + slot + r * %d;" % SLOTS)
+        w("(void)row;")
+        w("const tg_i64 q = (rs[r] & ~(tg_i64)%d) + (tg_i64)lane * %d;" % (ALIGN - 1, U))
+        w.open("if (q < re[r] && rs[r] < re[r])")
+        step("q", "rs[r]", "re[r]", "acc[r]")
+        w.close()
+        w.close()
+    else:
+        w("// first step of every row: every row's loads, then every row's gathers (none")
+        w("// behind a per-lane condition, so they issue back to back), then the sums")
+        w("tg_i64 fci[%d][%d]; double fcv[%d][%d];" % (R, U, R, U))
+        w("#pragma unroll")
+        w.open("for (int r = 0; r < %d; ++r)" % R)
+        w("const tg_i64 q = (rs[r] & ~(tg_i64)%d) + (tg_i64)lane * %d;" % (ALIGN - 1, U))
+        w("#pragma unroll")
+        w("for (int u = 0; u < %d; ++u) { fci[r][u] = 0; fcv[r][u] = 0.0; }" % U)
+        w.open("if (q < re[r] && rs[r] < re[r])")
+        if U % 2 == 0:
+            w.open("if (pair_ok && q + %d <= nnz)" % U)
+            for u in range(0, U, 2):
+                w("{ const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + q + %d));"
+                  " fci[r][%d] = a.x; fci[r][%d] = a.y; }" % (u, u, u + 1))
+                w("{ const tg_f64x2 b = __builtin_nontemporal_load((const tg_f64x2*)(data + q + %d));"
+                  " fcv[r][%d] = b.x; fcv[r][%d] = b.y; }" % (u, u, u + 1))
+            w.close()
+            w.open("else")
+        else:
+            w.open("")
+        for u in range(U):
+            w("fci[r][%d] = q + %d < nnz ? __builtin_nontemporal_load(indices + q + %d) : 0;" % (u, u, u))
+            w("fcv[r][%d] = q + %d < nnz ? __builtin_nontemporal_load(data + q + %d) : 0.0;" % (u, u, u))
+        w.close()
+        w.close()
+        w.close()
+        w.open("if (nnz > 0)")
+        w("double fxv[%d][%d]; bool fok[%d][%d];" % (R, U, R, U))
+        w("#pragma unroll")
+        w.open("for (int r = 0; r < %d; ++r)" % R)
+        w("const tg_i64 row = row0 + slot + r * %d;" % SLOTS)
+        w("(void)row;")
+        w("const tg_i64 q = (rs[r] & ~(tg_i64)%d) + (tg_i64)lane * %d;" % (ALIGN - 1, U))
+        w("#pragma unroll")
+        w.open("for (int u = 0; u < %d; ++u)" % U)
+        w("const tg_i64 pu = q + u;")
+        w("fok[r][u] = (pu >= rs[r]) & (pu < re[r]);")
+        w("const tg_i64 cu = fok[r][u] ? fci[r][u] : 0;")
+        w("fxv[r][u] = %s;" % _cexpr(gathered, _Env({row: "row", col: "cu"}, p="pu")))
+        w.close()
+        w.close()
+        w("#pragma unroll")
+        w.open("for (int r = 0; r < %d; ++r)" % R)
+        w("const tg_i64 row = row0 + slot + r * %d;" % SLOTS)
+        w("(void)row;")
+        w("#pragma unroll")
+        w.open("for (int u = 0; u < %d; ++u)" % U)
+        w("acc[r] = fok[r][u] ? acc[r] + %s : acc[r];"
+          % _value_with(plan, "fcv[r][u]", "fxv[r][u]", row, "fci[r][u]"))
+        w.close()
+        w.close()
+        w.close()
     w("// remaining steps (rows longer than %d nonzeros)" % (STEP - ALIGN + 1))
     w("#pragma unroll")
     w.open("for (int r = 0; r < %d; ++r)" % R)
