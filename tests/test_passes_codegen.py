@@ -479,8 +479,8 @@ def test_stream_tile_through_passes_and_ir():
 
 
 def test_lane_group_rows_load_before_any_gather():
-    """A lane group owning several rows of its tile (R > 1, as c2's schedule)
-    issues every row's first-step loads, then every row's gathers outside any
+    """A lane group owning several rows of its tile (1 < R, R U <= 8, as c2's
+    schedule) issues every row's first-step loads, then every row's gathers outside any
     per-lane condition (positions outside a row gather x[0] and are masked,
     under a uniform nnz > 0), then the sums; one row per lane group (c1's
     schedule) keeps the single guarded step."""
@@ -498,3 +498,8 @@ def test_lane_group_rows_load_before_any_gather():
     one = generate(standard_kernels()["spmv"], TUNED["c1"], "hip", write=False).source
     assert "every row's loads" not in one
     assert "// first step of every row in flight before any accumulation" in one
+    # past R U = 8 the operands of every row would not fit in registers: one step per row
+    big = generate(standard_kernels()["spmv"],
+                   Config(tile_size=256, threads_per_row=64, unroll=4, block_size=256), "hip",
+                   write=False).source
+    assert "every row's loads" not in big

@@ -1656,7 +1656,9 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w("acc[r] = 0.0;")
     w.close()
 
-    if R == 1:
+    # every row's first step held at once costs about 6 R U registers per lane: past
+    # R U = 8 that spills, so such schedules keep one guarded step per row
+    if R == 1 or R * U > 8:
         w("// first step of every row in flight before any accumulation")
         w("#pragma unroll")
         w.open("for (int r = 0; r < %d; ++r)" % R)
