@@ -166,6 +166,28 @@ def test_no_packed_fp32_in_generated_code(tmp_path):
         assert "scratch_" not in asm  # no register spills
 
 
+def test_tuned_schedules_do_not_spill(tmp_path):
+    """The schedule every BASELINE config is benchmarked with, and the no-alloc
+    schedule, keep all their values in registers: the code object's metadata
+    gives no private segment and no VGPR or SGPR spills."""
+    readelf = "/opt/rocm/llvm/bin/llvm-readelf"
+    if not os.path.exists(readelf):
+        pytest.skip("llvm-readelf not available")
+    from tilegen_amd.matrices import baseline_case
+    from tilegen_amd.schedules import NOALLOC_SCHEDULE, TUNED
+    todo = [(baseline_case(c).kernel, c, cfg) for c, cfg in TUNED.items()]
+    todo.append(("spmv", "noalloc", NOALLOC_SCHEDULE))
+    for kernel, label, cfg in todo:
+        gen = generate(standard_kernels()[kernel], cfg, "hip", outdir=str(tmp_path))
+        so, _ = compile_generated(gen, "hip", str(tmp_path))
+        notes = subprocess.run([readelf, "--notes", so[:-3] + ".co"], capture_output=True,
+                               text=True).stdout
+        meta = dict(re.findall(r"\.(private_segment_fixed_size|vgpr_spill_count|"
+                               r"sgpr_spill_count):\s+(\d+)", notes))
+        assert len(meta) == 3, (label, notes[:400])
+        assert all(v == "0" for v in meta.values()), (label, cfg.short(), meta)
+
+
 def test_noalloc_library_exports_its_header():
     """libtgna.so exports exactly what include/tilegen_noalloc.h declares and
     loads without a GPU."""
