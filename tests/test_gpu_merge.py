@@ -311,12 +311,15 @@ def _random_skewed(seed: int):
     return csr(M, N, indptr, indices, rng.uniform(-1, 1, size=indices.size))
 
 
-@pytest.mark.parametrize("cfg", STREAM_TEST_SCHEDULES[:4],
-                         ids=[schedule_id(c) for c in STREAM_TEST_SCHEDULES[:4]])
+_SKEWED_STREAM = STREAM_TEST_SCHEDULES[:4] + STREAM_TEST_SCHEDULES[-2:]
+
+
+@pytest.mark.parametrize("cfg", _SKEWED_STREAM, ids=[schedule_id(c) for c in _SKEWED_STREAM])
 def test_stream_random_skewed_matrices(cfg, hip_ready):
-    """24 seeded random skewed matrices (3,600 cut rows, 1,100 of them in more than
-    two pieces across the range sizes swept): every one meets the bar against
-    the oracle and SciPy, and a second launch onto NaNs gives the same bits."""
+    """24 seeded random skewed matrices (4,600 cut rows, 1,400 of them in more than
+    two pieces, across the six range sizes swept, two of them from blocks of 3
+    and 7 waves): every one meets the bar against the oracle and SciPy, and a
+    second launch onto NaNs gives the same bits."""
     for seed in range(24):
         A = _random_skewed(seed)
         print("[gpu] stream random seed=%d %s rows=%d nnz=%d" % (seed, cfg.short(), A.shape[0],

@@ -116,7 +116,8 @@ HYBRID_TEST_SCHEDULES: List[Config] = [
 # The same for stream ranges (an equal range of block x unroll nonzeros per
 # workgroup, rows summed from LDS): one wave (both row searches in one wave) and
 # sixteen, ranges of 64 to 8192 nonzeros, odd and even unroll, every lane-group
-# width tier.  The tile size is not used by this form.
+# width tier, and blocks of 3 and 7 waves (legal, though the tuner offers powers
+# of two only).  The tile size is not used by this form.
 STREAM_TEST_SCHEDULES: List[Config] = [
     Config(tile_size=64, threads_per_row=4, unroll=2, block_size=256, balance="stream"),
     Config(tile_size=64, threads_per_row=1, unroll=1, block_size=64, balance="stream"),
@@ -124,6 +125,8 @@ STREAM_TEST_SCHEDULES: List[Config] = [
     Config(tile_size=128, threads_per_row=8, unroll=8, block_size=1024, balance="stream"),
     Config(tile_size=8, threads_per_row=16, unroll=4, block_size=128, balance="stream"),
     Config(tile_size=256, threads_per_row=2, unroll=1, block_size=512, balance="stream"),
+    Config(tile_size=24, threads_per_row=8, unroll=2, block_size=192, balance="stream"),
+    Config(tile_size=224, threads_per_row=2, unroll=4, block_size=448, balance="stream"),
 ]
 
 
