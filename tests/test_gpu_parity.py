@@ -223,6 +223,10 @@ SPMM_SKEW_CFGS = [
     Config(tile_size=32, threads_per_row=8, unroll=2, vector_width=2, block_size=128),
     Config(tile_size=8, threads_per_row=64, unroll=4, vector_width=2, block_size=256),
     Config(tile_size=256, threads_per_row=4, unroll=1, vector_width=1, block_size=1024),
+    # lane-group counts that are not powers of two (3 and 40): the long rows' partial
+    # C-row slices are added by a tree over an odd count
+    Config(tile_size=12, threads_per_row=64, unroll=1, vector_width=1, block_size=192),
+    Config(tile_size=40, threads_per_row=8, unroll=2, vector_width=2, block_size=320),
 ]
 
 
