@@ -177,6 +177,11 @@ SKEW_CFGS = [
     Config(tile_size=64, threads_per_row=1, unroll=1, block_size=64),     # long = 8 nonzeros
     Config(tile_size=32, threads_per_row=4, unroll=3, block_size=256),
     Config(tile_size=16, threads_per_row=64, unroll=4, block_size=1024),
+    # workgroups of 3 and 5 waves: the waves' partial sums of a listed row are added in
+    # wave order over a count that is not a power of two; T96/TPR4/U2/B192 also takes the
+    # multi-row first step (two rows per lane group)
+    Config(tile_size=96, threads_per_row=4, unroll=2, block_size=192),
+    Config(tile_size=40, threads_per_row=8, unroll=2, block_size=320),
 ]
 
 
