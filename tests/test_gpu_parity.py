@@ -205,6 +205,9 @@ CHUNK_CFGS = [
     Config(tile_size=8, threads_per_row=64, unroll=1, vector_width=1, block_size=128),
     Config(tile_size=64, threads_per_row=4, unroll=8, vector_width=2, block_size=256),
     Config(tile_size=32, threads_per_row=1, unroll=16, vector_width=2, block_size=64),
+    # workgroups of 3 and 5 waves, whose lane groups share out listed rows' chunks
+    Config(tile_size=24, threads_per_row=8, unroll=4, vector_width=2, block_size=192),
+    Config(tile_size=80, threads_per_row=4, unroll=8, vector_width=2, block_size=320),
 ]
 
 
@@ -256,6 +259,7 @@ SDDMM_WIDE_CFGS = [
     Config(tile_size=16, threads_per_row=4, unroll=2, vector_width=2, block_size=256),
     Config(tile_size=8, threads_per_row=16, unroll=1, vector_width=1, block_size=128),
     Config(tile_size=64, threads_per_row=64, unroll=2, vector_width=2, block_size=1024),
+    Config(tile_size=12, threads_per_row=16, unroll=1, vector_width=1, block_size=192),
 ]
 
 
