@@ -1,0 +1,350 @@
+"""Hardware probes behind the measured ceilings of the CSR SpMV path on MI355X.
+
+These kernels are not part of the product path: they time one access pattern
+in isolation so that a kernel's time can be set against the floor of the loads
+it has to make.  Each probe reads a BASELINE matrix's own ``indices`` and
+``data``, rotates over enough input copies that every launch reads HBM, times
+every launch with dispatch-attached events (the same ``tg_time_launches`` as
+``bench.py``) and checks its own output against numpy.
+
+``flat`` makes a SpMV's loads with no rows at all: workgroup w takes the
+nonzeros [w CH, (w+1) CH), CH = BLK x U; lane t loads its U (index, value)
+pairs as 128-bit loads at positions 2 (k BLK + t) + h (k < U/2, h in {0, 1}),
+gathers ``x`` at each index, and SEG lanes sum their products into one output.
+The gather instruction for (k, h) therefore covers, for the 64 lanes of one
+wave, the items s = (2k + h) BLK + t of the range in the order the host laid
+them out.
+
+Orders (how the host lays out each range of CH nonzeros before upload):
+
+* ``matrix``: the matrix's own order;
+* ``b<S>``: sorted by ``col >> S`` (stable), then placed so that gather
+  instruction j of wave w takes the sorted items j BLK + 64 w ... + 63, that is
+  64 consecutive items of the sorted range.  This is the order a kernel would
+  reach by counting-sorting each range in LDS; the probe pays none of that
+  sort, so it bounds what such a kernel could gain;
+* ``line``: the same with S = 4 (one 128-byte line of ``x`` per key).
+
+Gather modes: ``x`` (``x[col]``), ``none`` (the index itself used as the
+operand, so the index loads stay live but nothing is gathered) and ``one``
+(``x[col & 7]``: every address in one line, so the gather's address work is
+kept and its line traffic removed).
+
+    python -m tilegen_amd.probes flat --case c1 --order matrix,b9,line \\
+        --shape 1024x4,1024x8 [--gather x,none,one] [--json out.json]
+    python -m tilegen_amd.probes --build          # compile every probe (no GPU)
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import hashlib
+import json
+import os
+import sys
+import time
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import numpy as np
+
+__all__ = ["flat_source", "flat_layout", "flat_expected", "gather_lines", "main"]
+
+_GATHER = {"x": "x[c]", "none": "(double)c", "one": "x[c & 7]"}
+
+
+def flat_source(name: str, blk: int, u: int, seg: int, gather: str) -> str:
+    """HIP source of one ``flat`` probe kernel (``extern "C"`` ``name``)."""
+    from .codegen import _HIP_PRELUDE
+    if u % 2 or u < 2 or blk % 64 or seg not in (1, 2, 4, 8, 16, 32, 64):
+        raise ValueError("flat probe needs an even U, a block of whole waves and SEG | 64")
+    ch = blk * u
+    lines = [_HIP_PRELUDE,
+             '#define TG_GATHER(c) (%s)' % _GATHER[gather],
+             'extern "C" __global__ __launch_bounds__(%d)' % blk,
+             "void %s(const tg_i64* __restrict__ indices, const double* __restrict__ data," % name,
+             "        const double* __restrict__ x, double* __restrict__ out, const tg_i64 nnz) {",
+             "  const tg_i64 p0 = (tg_i64)blockIdx.x * %d;" % ch,
+             "  const int cnt = (int)(nnz - p0 < %d ? nnz - p0 : %d);" % (ch, ch),
+             "  const int t = threadIdx.x;",
+             "  tg_i64 ci[%d]; double cv[%d];" % (u, u)]
+    for k in range(u // 2):
+        q = "2 * (%d + t)" % (k * blk)
+        lines += ["  {",
+                  "    const int q = %s;" % q,
+                  "    if (q + 1 < cnt) {",
+                  "      const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + p0 + q));",
+                  "      const tg_f64x2 b = __builtin_nontemporal_load((const tg_f64x2*)(data + p0 + q));",
+                  "      ci[%d] = a.x; ci[%d] = a.y; cv[%d] = b.x; cv[%d] = b.y;" % (2 * k, 2 * k + 1,
+                                                                              2 * k, 2 * k + 1),
+                  "    } else {",
+                  "      ci[%d] = q < cnt ? indices[p0 + q] : 0;" % (2 * k),
+                  "      cv[%d] = q < cnt ? data[p0 + q] : 0.0;" % (2 * k),
+                  "      ci[%d] = 0; cv[%d] = 0.0;" % (2 * k + 1, 2 * k + 1),
+                  "    }",
+                  "  }"]
+    lines.append("  double xv[%d];" % u)
+    for j in range(u):
+        lines.append("  { const tg_i64 c = ci[%d]; xv[%d] = TG_GATHER(c); }" % (j, j))
+    lines.append("  double acc = 0.0;")
+    for j in range(u):
+        lines.append("  acc += cv[%d] * xv[%d];" % (j, j))
+    lines += ["  acc = tg_segsum<%d>(acc);" % seg,
+              "  if (t %% %d == 0) out[((tg_i64)blockIdx.x * %d + t) / %d] = acc;" % (seg, blk, seg),
+              "}"]
+    return "\n".join(lines) + "\n"
+
+
+def _slot_of_sorted(blk: int, u: int) -> np.ndarray:
+    """pos[s]: the position in a range of CH = blk*u nonzeros that the flat
+    kernel's gather instruction j = s // blk, lane t = s % blk reads."""
+    s = np.arange(blk * u)
+    j, t = s // blk, s % blk
+    return 2 * ((j // 2) * blk + t) + (j % 2)
+
+
+def flat_layout(indices: np.ndarray, data: np.ndarray, blk: int, u: int, order: str
+                ) -> Tuple[np.ndarray, np.ndarray]:
+    """``indices``/``data`` laid out in ``order`` per range of blk*u nonzeros
+    (the last, partial range keeps the matrix order)."""
+    if order == "matrix":
+        return indices.copy(), data.copy()
+    shift = 4 if order == "line" else int(order[1:])
+    ch = blk * u
+    full = (len(indices) // ch) * ch
+    ind, val = indices.copy(), data.copy()
+    if full:
+        ki = indices[:full].reshape(-1, ch)
+        kv = data[:full].reshape(-1, ch)
+        srt = np.argsort(ki >> shift, axis=1, kind="stable")
+        si = np.take_along_axis(ki, srt, axis=1)
+        sv = np.take_along_axis(kv, srt, axis=1)
+        pos = _slot_of_sorted(blk, u)
+        oi = np.empty_like(ki)
+        ov = np.empty_like(kv)
+        oi[:, pos] = si
+        ov[:, pos] = sv
+        ind[:full] = oi.ravel()
+        val[:full] = ov.ravel()
+    return ind, val
+
+
+def flat_expected(ind: np.ndarray, val: np.ndarray, x: np.ndarray, blk: int, u: int, seg: int,
+                  gather: str) -> np.ndarray:
+    """What the flat kernel writes for the laid-out arrays."""
+    ch = blk * u
+    nnz = len(ind)
+    grid = -(-nnz // ch)
+    pi = np.zeros(grid * ch, dtype=np.int64)
+    pv = np.zeros(grid * ch)
+    pi[:nnz] = ind
+    pv[:nnz] = val
+    if gather == "x":
+        g = x[pi]
+    elif gather == "one":
+        g = x[pi & 7]
+    else:
+        g = pi.astype(np.float64)
+    prod = (pv * g).reshape(grid, u // 2, blk, 2)   # [range][pair k][lane t][half h]
+    lane = prod.sum(axis=(1, 3))                      # [range][lane]
+    return lane.reshape(grid, blk // seg, seg).sum(axis=2).ravel()
+
+
+def gather_lines(ind: np.ndarray, blk: int, u: int) -> float:
+    """Distinct 128-byte lines of ``x`` per gathered address, counted per
+    64-lane gather instruction of the flat kernel (the L1->L2 requests that
+    gather would make if no line were found in L1)."""
+    ch = blk * u
+    full = (len(ind) // ch) * ch
+    if not full:
+        return float("nan")
+    r = ind[:full].reshape(-1, u // 2, blk // 64, 64, 2) >> 4   # [range][k][wave][lane][h]
+    r = np.moveaxis(r, 4, 2).reshape(-1, 64)                     # one row per instruction
+    r = np.sort(r, axis=1)
+    distinct = 1 + (np.diff(r, axis=1) != 0).sum(axis=1)
+    return float(distinct.sum() / r.size)
+
+
+def _cache_dir() -> str:
+    from .verify import cache_dir
+    return cache_dir()
+
+
+def _code_object(name: str, src: str) -> bytes:
+    """hipRTC code object of ``src``, cached in the kernel cache by hash."""
+    from . import runtime as rt
+    from .verify import hiprtc_options
+    opts = hiprtc_options()
+    key = hashlib.sha1("\0".join([src] + opts).encode()).hexdigest()[:20]
+    path = os.path.join(_cache_dir(), "%s_%s.co" % (name, key))
+    if os.path.exists(path):
+        with open(path, "rb") as fh:
+            return fh.read()
+    code, _log = rt.rtc_compile(src, name + ".hip", opts)
+    tmp = path + ".tmp%d" % os.getpid()
+    with open(tmp, "wb") as fh:
+        fh.write(code)
+    os.replace(tmp, path)
+    return code
+
+
+def _function(name: str, src: str) -> int:
+    from . import runtime as rt
+    code = _code_object(name, src)
+    blob = ctypes.create_string_buffer(code, len(code))
+    mod, fn = ctypes.c_void_p(), ctypes.c_void_p()
+    rt.check(rt.lib().tg_module_load(blob, len(code), ctypes.byref(mod)), "tg_module_load")
+    rt.check(rt.lib().tg_module_function(mod, name.encode(), ctypes.byref(fn)),
+             "tg_module_function")
+    return int(fn.value)
+
+
+def _shapes(text: str) -> List[Tuple[int, int]]:
+    out = []
+    for part in text.split(","):
+        b, u = part.lower().split("x")
+        out.append((int(b), int(u)))
+    return out
+
+
+def _variants(orders: Sequence[str], shapes: Sequence[Tuple[int, int]],
+              gathers: Sequence[str], seg: int) -> List[Tuple[str, str, int, int, str]]:
+    """(kernel name, order, blk, u, gather); every order has a kernel of its
+    own name, so a rocprofv3 run tells them apart."""
+    out = []
+    for blk, u in shapes:
+        for g in gathers:
+            for o in (orders if g == "x" else ("matrix",)):
+                out.append(("probe_flat_%s_%s_b%du%d" % (g, o, blk, u), o, blk, u, g))
+    return out
+
+
+def build(orders=("matrix", "b9", "line"), shapes=((1024, 4), (1024, 8), (512, 8)),
+          gathers=("x", "none", "one"), seg: int = 4) -> int:
+    n = 0
+    for name, _o, blk, u, g in _variants(orders, shapes, gathers, seg):
+        _code_object(name, flat_source(name, blk, u, seg, g))
+        n += 1
+    return n
+
+
+def run_flat(case_id: str, orders: Sequence[str], shapes: Sequence[Tuple[int, int]],
+             gathers: Sequence[str], seg: int, warmup: int, iters: int, repeats: int,
+             control: bool) -> List[Dict[str, object]]:
+    from . import runtime as rt
+    from .matrices import baseline_case, baseline_operands, compulsory_bytes, make_baseline
+    from .profiling import bench_copies
+    A = make_baseline(case_id)
+    case = baseline_case(case_id)
+    if case.kernel != "spmv":
+        raise SystemExit("the flat probe takes an SpMV case")
+    M, N = A.shape
+    nnz = int(A.nnz)
+    x = baseline_operands("spmv", M, N, 1)["x"]
+    ind0 = A.indices.astype(np.int64)
+    val0 = A.data.astype(np.float64)
+    nbytes = compulsory_bytes("spmv", M, N, nnz)
+    copies = bench_copies(nbytes)
+    print("[probe] %s M=%d N=%d nnz=%d, %d copies" % (case_id, M, N, nnz, copies), flush=True)
+    variants = _variants(orders, shapes, gathers, seg)
+    layouts: Dict[Tuple[str, int, int], Tuple[list, np.ndarray, np.ndarray, float]] = {}
+    xs = [rt.DeviceBuffer(x) for _ in range(copies)]
+    records = []
+    timed: Dict[str, List[np.ndarray]] = {}
+    meta: Dict[str, Dict[str, object]] = {}
+    tuned = None
+    if control:
+        from .schedules import TUNED
+        from .variant import Variant
+        v = Variant("spmv", TUNED[case_id])
+        bufs = []
+        for c in range(copies):
+            b = {"indptr": rt.DeviceBuffer(A.indptr.astype(np.int64)),
+                 "indices": rt.DeviceBuffer(ind0), "data": rt.DeviceBuffer(val0),
+                 "x": xs[c], "y": rt.DeviceBuffer(nbytes=M * 8)}
+            bufs.append(b)
+        sets = [v.abi_values(A, b, {}, M, N, case.K, nnz) for b in bufs]
+        g, bl, lds = v.geometry(M, N, case.K, nnz)
+        tuned = (v.function(), g, bl, lds, sets, bufs, TUNED[case_id].short())
+    for _rep in range(repeats):
+        if tuned is not None:
+            fn, g, bl, lds, sets, _b, sched = tuned
+            kms, _ = rt.time_launches(fn, g, bl, lds, sets, warmup, iters)
+            timed.setdefault("tuned", []).append(kms)
+            meta["tuned"] = {"kernel": "spmv tuned " + sched, "order": "matrix"}
+            print("[probe] tuned %s: avg %.2f us median %.2f us" % (
+                sched, kms.mean() * 1e3, np.median(kms) * 1e3), flush=True)
+        for name, order, blk, u, g in variants:
+            key = (order, blk, u)
+            if key not in layouts:
+                ind, val = flat_layout(ind0, val0, blk, u, order)
+                dev = [(rt.DeviceBuffer(ind), rt.DeviceBuffer(val)) for _ in range(copies)]
+                layouts[key] = (dev, ind, val, gather_lines(ind, blk, u))
+            dev, ind, val, lpg = layouts[key]
+            fn = _function(name, flat_source(name, blk, u, seg, g))
+            ch = blk * u
+            grid = -(-nnz // ch)
+            out = rt.DeviceBuffer(nbytes=grid * (blk // seg) * 8)
+            sets = [[dev[c][0], dev[c][1], xs[c], out, nnz] for c in range(copies)]
+            kms, _ = rt.time_launches(fn, grid, blk, 0, sets, warmup, iters)
+            got = out.to_host(np.empty(grid * (blk // seg)))
+            exp = flat_expected(ind, val, x, blk, u, seg, g)
+            err = float(np.abs(got - exp).max() / max(np.abs(exp).max(), 1e-300))
+            out.free()
+            if not err <= 1e-12:
+                raise SystemExit("probe %s output check failed: rel err %.3e" % (name, err))
+            timed.setdefault(name, []).append(kms)
+            meta[name] = {"order": order, "block": blk, "unroll": u, "range": ch, "grid": grid,
+                          "gather": g, "lines_per_gather": round(lpg, 4), "err": err}
+            print("[probe] %-34s avg %.2f us median %.2f us (lines/gather %.3f, err %.1e)" % (
+                name, kms.mean() * 1e3, np.median(kms) * 1e3, lpg, err), flush=True)
+    for name, runs in timed.items():
+        rec = dict(meta[name])
+        rec.update({"name": name, "case": case_id,
+                    "us_avg": [round(float(k.mean()) * 1e3, 3) for k in runs],
+                    "us_median": [round(float(np.median(k)) * 1e3, 3) for k in runs],
+                    "launches": iters, "copies": copies})
+        records.append(rec)
+    return records
+
+
+def main(argv: Optional[Sequence[str]] = None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("probe", nargs="?", choices=["flat"], default="flat")
+    ap.add_argument("--build", action="store_true", help="compile the probes and exit")
+    ap.add_argument("--case", default="c1")
+    ap.add_argument("--order", default="matrix,b9,line")
+    ap.add_argument("--shape", default="1024x4,1024x8,512x8",
+                    help="BLOCKxU per probe (U nonzeros per lane, even)")
+    ap.add_argument("--gather", default="x,none,one")
+    ap.add_argument("--seg", type=int, default=4, help="lanes summed into one output")
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--iters", type=int, default=200)
+    ap.add_argument("--repeats", type=int, default=3, help="interleaved repeats")
+    ap.add_argument("--no-control", action="store_true",
+                    help="skip the tuned product kernel timed beside the probes")
+    ap.add_argument("--json", default=None, help="also write the records here")
+    args = ap.parse_args(argv)
+    orders = [o for o in args.order.split(",") if o]
+    for o in orders:
+        if o not in ("matrix", "line") and not (o[0] == "b" and o[1:].isdigit()):
+            raise SystemExit("bad order %r (matrix, line or b<shift>)" % o)
+    shapes = _shapes(args.shape)
+    gathers = [g for g in args.gather.split(",") if g]
+    if args.build:
+        t0 = time.time()
+        n = build(orders, shapes, gathers, args.seg)
+        print("built %d probe code objects in %.1fs" % (n, time.time() - t0))
+        return 0
+    recs = run_flat(args.case, orders, shapes, gathers, args.seg, args.warmup, args.iters,
+                    args.repeats, not args.no_control)
+    for r in recs:
+        print(json.dumps(r, separators=(",", ":")), flush=True)
+    if args.json:
+        with open(args.json, "w") as fh:
+            json.dump(recs, fh, indent=1)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
