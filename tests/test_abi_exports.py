@@ -54,6 +54,7 @@ def test_variant_library_exports_launch_abi(kernel, tmp_path):
                 if not s.startswith("launch_") or s == "launch_%s" % kernel]
     exported = _exported(so)
     assert not [s for s in declared if s not in exported]
+    assert "tgv_launch_async" in exported  # declared as one typedef per kernel
     runtime.lib()
     lib = ctypes.CDLL(so)
     lib.tgv_kernel_name.restype = ctypes.c_char_p
@@ -95,6 +96,50 @@ def test_header_signatures_match_generated_launchers():
     for name in standard_kernels():
         gen = generate(standard_kernels()[name], Config(), "hip", write=False)
         assert " ".join(gen.abi_signature.split()) == decls["launch_%s" % name], name
+
+
+def test_header_async_typedefs_match_generated_launchers():
+    """Each tgv_launch_async_<name>_fn typedef in the header is the parameter
+    list of the generated tgv_launch_async of that kernel (the stream, then the
+    launch_<name> arguments), token for token, and every variant library
+    exports tgv_launch_async."""
+    text = open(os.path.join(ROOT, "include", "tilegen_launch.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {m.group(1): " ".join(m.group(2).split())
+             for m in re.finditer(r"typedef int \(\*tgv_launch_async_([a-z_]+)_fn\)\(([^)]*)\)",
+                                  text)}
+    assert sorted(decls) == sorted(standard_kernels())
+    for name in standard_kernels():
+        gen = generate(standard_kernels()[name], Config(), "hip", write=False)
+        m = re.search(r"int tgv_launch_async\(([^)]*)\)", gen.host_source)
+        assert m, name
+        assert " ".join(m.group(1).split()) == decls[name], name
+        params = ", ".join("%s %s" % a for a in gen.abi_args)
+        assert decls[name] == " ".join(("void* stream, " + params).split()), name
+
+
+def test_launchers_pass_no_dynamic_lds(tmp_path):
+    """Every generated kernel declares its LDS statically, so the launch asks for
+    no dynamic LDS on top of it (passing the static size again would reserve it
+    twice per workgroup and halve the workgroups a CU can hold)."""
+    from tilegen_amd.matrices import baseline_case
+    from tilegen_amd.schedules import NOALLOC_SCHEDULE, TUNED
+    todo = [(baseline_case(c).kernel, cfg) for c, cfg in TUNED.items()]
+    todo += [("spmv", NOALLOC_SCHEDULE),
+             ("spmv", Config(tile_size=64, threads_per_row=4, unroll=2, block_size=256,
+                             balance="nnz"))]
+    runtime.lib()
+    for kernel, cfg in todo:
+        gen = generate(standard_kernels()[kernel], cfg, "hip", outdir=str(tmp_path))
+        so, _ = compile_generated(gen, "hip", str(tmp_path))
+        assert "__shared__" in gen.source or gen.geometry.lds_bytes == 0, cfg.short()
+        assert "extern __shared__" not in gen.source
+        lib = ctypes.CDLL(so)
+        g, b, l = ctypes.c_int64(), ctypes.c_int32(), ctypes.c_int32(-1)
+        lib.tgv_geometry.argtypes = [ctypes.c_int64] * 4 + [ctypes.c_void_p] * 3
+        assert lib.tgv_geometry(100000, 100000, 64, 1600000, ctypes.byref(g), ctypes.byref(b),
+                                ctypes.byref(l)) == 0
+        assert l.value == 0, (cfg.short(), l.value)
 
 
 def test_runtime_error_reporting_without_device():

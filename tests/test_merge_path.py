@@ -53,8 +53,9 @@ def _ends(qs, passed):
     return f, (63 if f is None else (f - 1 if f > 0 else None))
 
 
-def mp_search(indptr, R: int, t: int, X: int):
-    """Lane-for-lane model of ``tg_mp_search``: (answer, rounds, probed rows)."""
+def mp_search(indptr, R: int, t: int, X: int, base: int = 0):
+    """Lane-for-lane model of ``tg_mp_search``: (answer, rounds, probed rows);
+    items are counted from ``base`` = indptr[0]."""
     g = int(float(t) * (float(R) / float(X))) if X > 0 else 0
     qs = first_probes(g)
     lo, hi, rounds, probed = 0, R, 0, set()
@@ -62,7 +63,7 @@ def mp_search(indptr, R: int, t: int, X: int):
         rounds += 1
         qs = [min(max(q, lo), hi) for q in qs]
         probed.update(qs)
-        f, fa = _ends(qs, [q + int(indptr[q]) >= t for q in qs])
+        f, fa = _ends(qs, [q + int(indptr[q]) - base >= t for q in qs])
         b = qs[f] if f is not None else hi
         a = qs[fa] if fa is not None else lo - 1
         lo, hi = a + 1, b
@@ -73,14 +74,17 @@ def mp_search(indptr, R: int, t: int, X: int):
 
 
 def lower_bound(indptr, R: int, t: int) -> int:
-    f = np.arange(R + 1, dtype=np.int64) + np.asarray(indptr[:R + 1], dtype=np.int64)
+    f = np.arange(R + 1, dtype=np.int64) + np.asarray(indptr[:R + 1], dtype=np.int64) \
+        - int(indptr[0])
     return min(int(np.searchsorted(f, t, side="left")), R)
 
 
 def partition(indptr, M: int, G: int, cap: int = cg.MERGE_CAP):
     """The emitter's per-workgroup window set-up for every workgroup: a list of
-    (rows summed whole, pieces) with pieces as (row, begin, end, wf, wl, w)."""
-    nnz = int(indptr[M])
+    (rows summed whole, pieces) with pieces as (row, begin, end, wf, wl, w).
+    Items count from pbase = indptr[0] (a block of rows of a larger matrix)."""
+    pbase = int(indptr[0])
+    nnz = int(indptr[M]) - pbase
     X = M + nnz
     D = (X + G - 1) // G if X > G else 1
     ip = lambda r: int(indptr[r]) if r >= 0 else 0  # noqa: E731
@@ -88,11 +92,12 @@ def partition(indptr, M: int, G: int, cap: int = cg.MERGE_CAP):
     for w in range(G):
         t0 = min(w * D, X)
         t1 = min(t0 + D, X)
-        r0 = 0 if w == 0 else mp_search(indptr, M, t0, X)[0]
-        r1 = M if w == G - 1 else mp_search(indptr, M, t1, X)[0]
+        r0 = 0 if w == 0 else mp_search(indptr, M, t0, X, pbase)[0]
+        r1 = M if w == G - 1 else mp_search(indptr, M, t1, X, pbase)[0]
         s2, s3, s4, s5 = ip(r0 - 1), ip(r0), ip(r1 - 1), ip(r1)
-        pc_in = r0 > 0 and s3 - s2 > D and (r0 - 1 + s3 - 1) // D < cap and r0 - 1 + s3 > t0
-        pc_out = r1 > r0 and s5 - s4 > D and (r1 - 1 + s5 - 1) // D < cap
+        pc_in = (r0 > 0 and s3 - s2 > D and (r0 - 1 + s3 - pbase - 1) // D < cap
+                 and r0 - 1 + s3 - pbase > t0)
+        pc_out = r1 > r0 and s5 - s4 > D and (r1 - 1 + s5 - pbase - 1) // D < cap
         r_own = r1 - 1 if pc_out else r1
         pieces = []
         for k, on in ((0, pc_in), (1, pc_out)):
@@ -100,9 +105,9 @@ def partition(indptr, M: int, G: int, cap: int = cg.MERGE_CAP):
                 continue
             row = r0 - 1 if k == 0 else r1 - 1
             pb, pe = (s2, s3) if k == 0 else (s4, s5)
-            c0 = t0 - row if k == 0 and t0 - row > pb else pb
-            c1 = min(t1 - row, pe)
-            pieces.append((row, c0, c1, (row + pb) // D, (row + pe - 1) // D, w))
+            c0 = t0 - row + pbase if k == 0 and t0 - row + pbase > pb else pb
+            c1 = min(t1 - row + pbase, pe)
+            pieces.append((row, c0, c1, (row + pb - pbase) // D, (row + pe - 1 - pbase) // D, w))
         out.append((range(r0, r_own), pieces, D))
     return out
 
@@ -140,7 +145,7 @@ def check_partition(indptr, M: int, G: int, cap: int = cg.MERGE_CAP) -> dict:
         if r not in cut:
             assert whole[r] == 1, (r, whole[r])
             if lens[r] > D:  # a long row kept whole: its windows reach past the scratch
-                assert (r + int(indptr[r + 1]) - 1) // D >= cap
+                assert (r + int(indptr[r + 1]) - int(indptr[0]) - 1) // D >= cap
     return {"D": D, "cut": len(cut), "max_pieces": max((len(v) for v in cut.values()), default=0)}
 
 
@@ -159,12 +164,16 @@ def _cases():
 
 @pytest.mark.parametrize("T", [1, 4, 16, 64, 1024])
 def test_partition_covers_every_nonzero_once(T):
+    """Also as a block of rows of a larger matrix (indptr[0] > 0, odd and even)."""
     seen_cut = 0
     for label, A in _cases():
         M = A.shape[0]
         G = max(1, -(-M // T))
         info = check_partition(A.indptr, M, G)
         seen_cut += info["cut"]
+        for off in (1, 6):
+            view = check_partition(np.asarray(A.indptr, dtype=np.int64) + off, M, G)
+            assert view == info, (label, off)
     if T <= 64:  # a window per 64 rows or fewer: the long rows above are cut
         assert seen_cut > 0
 
@@ -219,7 +228,7 @@ def test_merge_source_and_refusals():
     cfg = Config(tile_size=64, threads_per_row=8, unroll=2, block_size=512, balance="nnz")
     for k in ("spmv", "fused_spmv_axpy"):
         g = cg.generate(ks[k], cfg, backend="hip", write=False)
-        assert "tg_mp_search(indptr, row_lim, t0, X)" in g.source
+        assert "tg_mp_search(indptr, row_lim, t0, X, pbase)" in g.source
         assert "tg_mp_commit(tg_part, wdx, wf, wl, t, &tot)" in g.source
         tiling = [e for e in cg._passes.run_pipeline(ks[k], cfg, backend="hip").pass_log
                   if e["pass"] == "tiling"][0]
@@ -242,11 +251,12 @@ def test_merge_source_and_refusals():
 # --------------------------------------------------------------------------- #
 # hybrid tiles: row tiles plus long-row workgroups over equal nonzero ranges
 # --------------------------------------------------------------------------- #
-def _row_at(indptr, R, P, X):
-    """``tg_mp_row`` lane for lane: the row holding nonzero P with its bounds,
-    and the number of probe rounds it took."""
-    qs = first_probes(int(float(P) * (float(R) / float(X))))
-    lo, hi, vlo, vhi = 0, R, 0, X
+def _row_at(indptr, R, P, pb, pe):
+    """``tg_mp_row`` lane for lane: the row holding nonzero P, pb <= P < pe =
+    indptr[R], pb = indptr[0], with its bounds, and the number of probe rounds
+    it took."""
+    qs = first_probes(int(float(P - pb) * (float(R) / float(pe - pb))))
+    lo, hi, vlo, vhi = 0, R, pb, pe
     rounds = 0
     while True:
         rounds += 1
@@ -263,14 +273,28 @@ def _row_at(indptr, R, P, X):
         qs = [lo + 1 + l * s for l in range(64)]
 
 
+def _range(indptr, M: int, CH: int, e: int):
+    """Range e's positions [p0, p1): CH from (indptr[0] & ~1) + e CH, clipped to
+    [indptr[0], indptr[M])."""
+    pbase, pend = int(indptr[0]), int(indptr[M])
+    pa = (pbase & ~1) + e * CH
+    return max(pa, pbase), min(pa + CH, pend)
+
+
+def _ranges(indptr, M: int, CH: int) -> int:
+    """NR: the ranges the rows' nonzeros meet."""
+    pbase, pend = int(indptr[0]), int(indptr[M])
+    return -(-(pend - (pbase & ~1)) // CH) if pend > pbase else 0
+
+
 def hybrid_listed(indptr, M: int, CH: int, e: int):
     """The long rows range e lists, as (row, start, end): the distinct rows
     longer than CH / 2 among those holding nonzeros p0, p0 + CH / 2 (p1 - 1 when
     that lies past the range) and p1 - 1."""
-    nnz = int(indptr[M])
+    pbase, pend = int(indptr[0]), int(indptr[M])
     LH = CH // 2
-    p0, p1 = e * CH, min(e * CH + CH, nnz)
-    found = [_row_at(indptr, M, P, nnz)[:3]
+    p0, p1 = _range(indptr, M, CH, e)
+    found = [_row_at(indptr, M, P, pbase, pend)[:3]
              for P in (p0, p0 + LH if p0 + LH < p1 else p1 - 1, p1 - 1)]
     out = []
     for k, (r, rs, re) in enumerate(found):
@@ -279,26 +303,37 @@ def hybrid_listed(indptr, M: int, CH: int, e: int):
     return out
 
 
-def hybrid_pieces(indptr, M: int, CH: int, cap: int = cg.MERGE_CAP):
-    """The long-row workgroups as the emitter writes them: for every range e,
-    the (row, begin, end, ef, el, e, cut) pieces it sums, and the number of
-    rows it listed."""
-    nnz = int(indptr[M])
-    GL = -(-nnz // CH) if nnz > 0 else 0
+def hybrid_pieces(indptr, M: int, CH: int, cap: int = cg.MERGE_CAP, nnz=None):
+    """The long-row workgroups as the emitter writes them, for a launch with
+    ``nnz`` (default: the rows' own count): for every range e that exists (the
+    first NL = min(NR, GL), GL = floor(nnz / CH) + 1), the (row, begin, end, ef,
+    el, e, cut) pieces it sums (the last range's piece of the row holding its
+    last position runs to the row's end), the number of rows it listed, and
+    the long rows the row tiles keep (their first range does not exist)."""
+    pbase = int(indptr[0])
+    pal = pbase & ~1
+    if nnz is None:
+        nnz = int(indptr[M]) - pbase
+    GL = max(0, nnz) // CH + 1
+    NL = min(_ranges(indptr, M, CH), GL)
     out, listed = [], []
-    for e in range(GL):
-        p0, p1 = e * CH, min(e * CH + CH, nnz)
+    for e in range(NL):
+        p0, p1 = _range(indptr, M, CH, e)
+        last = e == NL - 1
         rows = hybrid_listed(indptr, M, CH, e)
         listed.append(len(rows))
         for row, rs, re in rows:
-            ef, el = rs // CH, (re - 1) // CH
+            ef, el = (rs - pal) // CH, min((re - 1 - pal) // CH, NL - 1)
             cut = el > ef and el < cap
             if not cut and ef != e:
                 continue
             q0 = max(p0, rs) if cut else rs
-            q1 = min(p1, re) if cut else re
+            q1 = (re if last else min(p1, re)) if cut else re
             out.append((row, q0, q1, ef, el, e, cut))
-    return out, listed
+    lens = np.diff(np.asarray(indptr[:M + 1], dtype=np.int64))
+    starts = np.asarray(indptr[:M], dtype=np.int64)
+    kept = set(np.nonzero((lens > CH // 2) & ((starts - pal) // CH >= NL))[0].tolist())
+    return out, listed, kept
 
 
 def test_row_search_finds_the_row_holding_a_nonzero():
@@ -311,7 +346,7 @@ def test_row_search_finds_the_row_holding_a_nonzero():
             continue
         for t in sorted(set([0, nnz - 1, nnz // 2] + list(np.random.default_rng(1).integers(
                 0, nnz, size=100)))):
-            r, rs, re, rounds = _row_at(ip, M, int(t), nnz)
+            r, rs, re, rounds = _row_at(ip, M, int(t), 0, nnz)
             assert r == int(np.searchsorted(ip, t, side="right")) - 1, (label, t)
             assert (rs, re) == (int(ip[r]), int(ip[r + 1])) and rs <= t < re
             assert rounds <= 2 + int(np.ceil(np.log(max(M, 2)) / np.log(63))), (label, t, rounds)
@@ -325,7 +360,7 @@ def test_row_search_with_empty_rows_everywhere():
     ip = np.concatenate([[0], np.cumsum(lens)])
     nnz = int(ip[-1])
     for t in range(nnz):
-        r, rs, re, _ = _row_at(ip, len(lens), t, nnz)
+        r, rs, re, _ = _row_at(ip, len(lens), t, 0, nnz)
         assert lens[r] > 0 and rs <= t < re and (rs, re) == (ip[r], ip[r + 1])
 
 
@@ -339,12 +374,14 @@ def test_ranges_list_every_long_row_meeting_them(CH):
         ip = np.asarray(A.indptr, dtype=np.int64)
         M, nnz = A.shape[0], int(ip[-1])
         lens = np.diff(ip)
-        for e in range(-(-nnz // CH) if nnz else 0):
-            p0, p1 = e * CH, min(e * CH + CH, nnz)
-            want = [int(r) for r in np.nonzero((lens > LH) & (ip[1:] > p0) & (ip[:-1] < p1))[0]]
-            got = hybrid_listed(ip, M, CH, e)
-            assert [r for r, _, _ in got] == want and len(got) <= 3, (label, CH, e)
-            assert all((rs, re) == (int(ip[r]), int(ip[r + 1])) for r, rs, re in got)
+        for off in (0, 1, CH + 5):
+            v = ip + off
+            for e in range(_ranges(v, M, CH)):
+                p0, p1 = _range(v, M, CH, e)
+                want = [int(r) for r in np.nonzero((lens > LH) & (v[1:] > p0) & (v[:-1] < p1))[0]]
+                got = hybrid_listed(v, M, CH, e)
+                assert [r for r, _, _ in got] == want and len(got) <= 3, (label, CH, e, off)
+                assert all((rs, re) == (int(v[r]), int(v[r + 1])) for r, rs, re in got)
 
 
 @pytest.mark.parametrize("CH", [128, 512, 2048, 4096])
@@ -354,17 +391,21 @@ def test_hybrid_long_rows_summed_once(CH):
     from its first to its last), no range lists more than 3 such rows (the
     kernel's list holds 8), and no range holds two pieces of one kind."""
     LH = CH // 2
-    for label, A in _cases():
+    for label, A, ip, nnz in _hybrid_launches(CH):
         M = A.shape[0]
-        pieces, listed = hybrid_pieces(A.indptr, M, CH)
+        pieces, listed, kept = hybrid_pieces(ip, M, CH, nnz=nnz)
         assert max(listed, default=0) <= 3, (label, max(listed))
         lens = np.diff(A.indptr)
         by_row = {}
         for p in pieces:
             by_row.setdefault(p[0], []).append(p)
-        assert set(by_row) == set(np.nonzero(lens > LH)[0].tolist()), label
+        assert not set(by_row) & kept, label
+        assert set(by_row) | kept == set(np.nonzero(lens > LH)[0].tolist()), label
+        own = int(ip[M] - ip[0])
+        if nnz >= own:
+            assert not kept, label  # nnz covers the rows: every long row has its ranges
         for row, ps in by_row.items():
-            rs, re = int(A.indptr[row]), int(A.indptr[row + 1])
+            rs, re = int(ip[row]), int(ip[row + 1])
             if len(ps) == 1 and not ps[0][6]:
                 assert (ps[0][1], ps[0][2]) == (rs, re)
                 continue
@@ -381,15 +422,28 @@ def test_hybrid_long_rows_summed_once(CH):
                 kinds[k] = p[0]
 
 
+def _hybrid_launches(CH):
+    """(label, matrix, indptr, nnz) launches: the cases as given, as blocks of a
+    larger matrix at odd and even offsets, and with nnz too large, zero and too
+    small."""
+    for label, A in _cases():
+        ip = np.asarray(A.indptr, dtype=np.int64)
+        own = int(ip[-1] - ip[0])
+        yield label, A, ip, own
+        for off in (1, 4, CH + 3):
+            for nnz in (own, own + 3 * CH, 0, own // 3):
+                yield "%s+%d/%d" % (label, off, nnz), A, ip + off, nnz
+
+
 def test_hybrid_source_and_geometry():
     from tilegen_amd import dsl
     ks = dsl.standard_kernels()
     cfg = Config(tile_size=64, threads_per_row=8, unroll=2, block_size=512, balance="hybrid")
     g = cg.generate(ks["spmv"], cfg, backend="hip", write=False)
-    assert "tg_mp_row(indptr, row_end, P, nnz, &rs, &re)" in g.source
-    assert "(nnz + 2048 - 1) / 2048" in g.host_source
+    assert "tg_mp_row(indptr, row_end, P, pbase, pend, &rs, &re)" in g.source
+    assert "*grid += (nnz > 0 ? nnz : 0) / 2048 + 1;" in g.host_source
     assert g.geometry.grid(100000, 794591) == 1563 + 388
-    assert g.geometry.grid(0, 5) == 0 and g.geometry.grid(10, 0) == 1
+    assert g.geometry.grid(0, 5) == 0 and g.geometry.grid(10, 0) == 2
     assert cfg.short().endswith("/hybrid")
 
 
@@ -397,7 +451,7 @@ def test_hybrid_rows_past_the_scratch_stay_whole():
     """With a scratch of 4 ranges, a long row reaching range 4 or later is summed
     whole by its first range and by no other; one within the first 4 is cut."""
     A = ragged(12, 300, 4000, 3, long_rows=[(2, 300), (250, 900)])
-    pieces, _ = hybrid_pieces(A.indptr, 300, 128, cap=4)
+    pieces, _, _ = hybrid_pieces(A.indptr, 300, 128, cap=4)
     by_row = {}
     for p in pieces:
         by_row.setdefault(p[0], []).append(p)
@@ -405,3 +459,11 @@ def test_hybrid_rows_past_the_scratch_stay_whole():
     assert len(by_row[250]) == 1 and not by_row[250][0][6]
     rs, re = int(A.indptr[250]), int(A.indptr[251])
     assert by_row[250][0][1:3] == (rs, re) and by_row[250][0][5] == rs // 128
+    # the same rows as a block of a larger matrix at an odd offset: ranges count from
+    # the even position below indptr[0]
+    off = 129
+    pieces, _, _ = hybrid_pieces(np.asarray(A.indptr) + off, 300, 128, cap=4)
+    by_row = {}
+    for p in pieces:
+        by_row.setdefault(p[0], []).append(p)
+    assert len(by_row[250]) == 1 and by_row[250][0][5] == (rs + off - 128) // 128

@@ -475,19 +475,19 @@ def test_stream_tile_through_passes_and_ir():
     assert cfg.hash() != plain.hash() and "balance" not in plain.to_dict()
     gen = generate(standard_kernels()["spmv"], cfg, "hip", write=False)
     assert gen.geometry.stream and gen.geometry.nnz_chunk == 2048
-    assert "grid = ceil(nnz / 2048)" in gen.source
+    assert "grid = floor(nnz / 2048) + 1" in gen.source
 
 
 def test_lane_group_rows_load_before_any_gather():
     """A lane group owning several rows of its tile (1 < R, R U <= 8, as c2's
     schedule) issues every row's first-step loads, then every row's gathers outside any
     per-lane condition (positions outside a row gather x[0] and are masked,
-    under a uniform nnz > 0), then the sums; one row per lane group (c1's
-    schedule) keeps the single guarded step."""
+    under a uniform ghi > glo: the tile holds nonzeros), then the sums; one row
+    per lane group (c1's schedule) keeps the single guarded step."""
     from tilegen_amd.schedules import TUNED
     src = generate(standard_kernels()["spmv"], TUNED["c2"], "hip", write=False).source
     loads = src.index("// first step of every row: every row's loads")
-    guard = src.index("if (nnz > 0) {", loads)
+    guard = src.index("if (ghi > glo) {", loads)
     gather = src.index("fxv[r][u] = x[cu];", guard)
     sums = src.index("acc[r] = fok[r][u] ?", gather)
     rest = src.index("// remaining steps", sums)

@@ -3,22 +3,32 @@ model: which rows each range of nonzeros writes, which row pieces it commits
 and which rows it sums whole, replayed from the same rules the emitted kernel
 follows (``codegen._hip_stream_reduce``).
 
-Range e holds nonzeros [e CH, (e+1) CH) and owns the rows from the row holding
-its first nonzero (row 0 for e = 0) up to the row holding the next range's
-first nonzero (M for the last range).  For every matrix below the model checks:
+The rows' nonzeros are the positions [pbase, pend) = [indptr[0], indptr[M]):
+indptr[0] may be nonzero (a block of rows of a larger matrix).  Range e stages
+the positions [pa, pa + CH), pa = (pbase & ~1) + e CH, clipped to [p0, ps)
+inside [pbase, pend), and owns the rows from the row holding p0 (row 0 for
+e = 0) up to the row holding the next range's first position.  The grid comes
+from the launch's nnz (floor(nnz / CH) + 1 workgroups), so only the first
+NL = min(NR, grid) ranges exist: the last of them owns every row up to M and
+sums, with its own loads, what lies past its staged positions (nothing when
+nnz covers the rows' nonzeros).  For every matrix below the model checks:
 
 * every row is finished exactly once: written whole by the one range that owns
   it, or combined from pieces, or (past the scratch) summed whole by its first
   range;
-* a combined row has exactly one piece in each range it spans, the pieces are
-  disjoint and cover its nonzeros in range order, and their slots lie inside the
-  scratch;
-* a row written whole is covered by the owning range's own products.
+* a combined row has exactly one piece in each range it spans (its last range
+  clamped to NL - 1), the pieces are disjoint and cover its nonzeros in range
+  order, and their slots lie inside the scratch;
+* a row written whole is covered by the owning range's own positions;
+* the staged positions of the ranges are disjoint, lie inside [pbase, pend),
+  and only the last range reads past them.
 
 The matrices put the rules at their edges: empty rows before, between and after
 the nonzeros, rows ending exactly at a range boundary, one row holding every
 nonzero, no nonzeros at all, a count of nonzeros that is a multiple of the range,
-and a scratch so small that long rows take the whole-row path.
+a scratch so small that long rows take the whole-row path, the same rows as a
+block of a larger matrix (indptr[0] odd and even), and launches whose nnz is
+exact, too large, zero or too small.
 """
 
 from __future__ import annotations
@@ -35,40 +45,54 @@ from tilegen_amd.dsl import standard_kernels
 
 
 def _row_holding(indptr, p):
-    """The row r with indptr[r] <= p < indptr[r + 1] (what tg_mp_row returns)."""
+    """The row r with indptr[r] <= p < indptr[r + 1] (what tg_st_row returns)."""
     return bisect.bisect_right(indptr, p) - 1
 
 
-def stream_split(indptr, CH, cap=cg.MERGE_CAP):
-    """Replay the kernel's decisions.  Returns (writes, pieces, whole, grid):
+def stream_split(indptr, CH, cap=cg.MERGE_CAP, nnz=None):
+    """Replay the kernel's decisions for a launch with ``nnz`` (default: the
+    rows' own count).  Returns (writes, pieces, whole, grid, staged):
     writes[r] = list of (range, lo, hi) covered by a whole-row write, pieces[r] =
     list of (range, lo, hi, slot) committed, whole[r] = ranges that sum r with
-    their own loads."""
+    their own loads, staged = (range, lo, hi, tail) per existing range."""
     indptr = [int(v) for v in indptr]
-    M, nnz = len(indptr) - 1, indptr[-1]
-    G = 0 if M == 0 else max(1, -(-nnz // CH))
-    writes, pieces, whole = defaultdict(list), defaultdict(list), Counter()
-    for e in range(G):
-        p0, p1 = e * CH, min(e * CH + CH, nnz)
+    M = len(indptr) - 1
+    if M == 0:
+        return defaultdict(list), defaultdict(list), Counter(), 0, []
+    pbase, pend = indptr[0], indptr[M]
+    if nnz is None:
+        nnz = pend - pbase
+    G = max(0, nnz) // CH + 1
+    pal = pbase & ~1
+    NR = -(-(pend - pal) // CH) if pend > pbase else 1
+    NL = min(NR, G)
+    writes, pieces, whole, staged = defaultdict(list), defaultdict(list), Counter(), []
+    for e in range(NL):
+        last = e == NL - 1
+        pa = pal + e * CH
+        p0, ps = max(pa, pbase), min(pa + CH, pend)
+        p1 = pend if last else ps
+        staged.append((e, p0, ps, last and p1 > ps))
         if e == 0:
-            ra, ra_s, ra_e = 0, 0, 0
+            ra, ra_s, ra_e = 0, pbase, pbase
         else:
             ra = _row_holding(indptr, p0)
             ra_s, ra_e = indptr[ra], indptr[ra + 1]
-        if p1 < nnz:
+        if p1 < pend:
             rb = _row_holding(indptr, p1)
             rb_s, rb_e = indptr[rb], indptr[rb + 1]
         else:
-            rb, rb_s, rb_e = M, nnz, nnz
+            rb, rb_s, rb_e = M, pend, pend
         ra_cut = e > 0 and ra < rb and ra_s < p0
         if ra_cut:
-            ef, el = ra_s // CH, (ra_e - 1) // CH
-            assert el == e
-            if el < cap:
+            ef = (ra_s - pal) // CH
+            assert min((ra_e - 1 - pal) // CH, NL - 1) == e
+            if e < cap:
                 pieces[ra].append((e, p0, ra_e, 2 * e + (1 if e == ef else 0)))
         if rb < M and rb_s < p1:
-            ef, el = rb_s // CH, (rb_e - 1) // CH
+            ef, el = (rb_s - pal) // CH, min((rb_e - 1 - pal) // CH, NL - 1)
             if el < cap:
+                assert rb_e > ps and not last
                 pieces[rb].append((e, max(rb_s, p0), p1, 2 * e + (1 if e == ef else 0)))
             elif ef == e:
                 whole[rb] += 1
@@ -78,14 +102,24 @@ def stream_split(indptr, CH, cap=cg.MERGE_CAP):
             st, en = max(indptr[r], p0), indptr[r + 1]
             assert p0 <= st <= en <= p1 or (st == en), (e, r, st, en, p0, p1)
             writes[r].append((e, st, en))
-    return writes, pieces, whole, G
+    return writes, pieces, whole, G, staged
 
 
-def check_split(indptr, CH, cap=cg.MERGE_CAP):
-    writes, pieces, whole, G = stream_split(indptr, CH, cap)
+def check_split(indptr, CH, cap=cg.MERGE_CAP, nnz=None):
+    writes, pieces, whole, G, staged = stream_split(indptr, CH, cap, nnz)
+    indptr = [int(v) for v in indptr]
     M = len(indptr) - 1
+    if M == 0:
+        return G
+    pbase, pend = indptr[0], indptr[M]
+    pal = pbase & ~1
+    NL = len(staged)
+    for a, b in zip(staged, staged[1:]):
+        assert a[2] == b[1] and not a[3], (a, b)   # disjoint, in order, no tail but the last
+    assert staged[0][1] == pbase and staged[-1][2] <= pend
+    assert all(pbase <= lo <= hi <= pend for _e, lo, hi, _t in staged)
     for r in range(M):
-        s, t = int(indptr[r]), int(indptr[r + 1])
+        s, t = indptr[r], indptr[r + 1]
         ways = (len(writes[r]) > 0) + (len(pieces[r]) > 0) + (whole[r] > 0)
         assert ways == 1, "row %d finished %d ways" % (r, ways)
         if writes[r]:
@@ -94,9 +128,9 @@ def check_split(indptr, CH, cap=cg.MERGE_CAP):
             assert (lo, hi) == (s, t) or s == t, (r, lo, hi, s, t)
         elif whole[r]:
             assert whole[r] == 1
-            assert (t - 1) // CH >= cap
+            assert min((t - 1 - pal) // CH, NL - 1) >= cap
         else:
-            wf, wl = s // CH, (t - 1) // CH
+            wf, wl = (s - pal) // CH, min((t - 1 - pal) // CH, NL - 1)
             assert wl > wf and wl < cap
             es = [p[0] for p in pieces[r]]
             assert sorted(es) == list(range(wf, wl + 1)), (r, es, wf, wl)
@@ -107,6 +141,17 @@ def check_split(indptr, CH, cap=cg.MERGE_CAP):
             assert all(0 <= slot < 2 * cap for *_x, slot in pieces[r])
             assert len({slot for *_x, slot in pieces[r]}) == len(pieces[r])
     return G
+
+
+def _views(ip, CH):
+    """The same rows as a block of a larger matrix: indptr shifted by offsets of
+    both parities, with launches whose nnz is exact, too large, zero and too
+    small."""
+    ip = np.asarray(ip, dtype=np.int64)
+    own = int(ip[-1] - ip[0]) if len(ip) > 1 else 0
+    for off in (0, 1, 2, 7, CH + 3):
+        for nnz in (own, own + 5 * CH + 1, 0, own // 3):
+            yield ip + off, nnz
 
 
 def _indptr(lengths):
@@ -130,7 +175,9 @@ def test_edge_layouts(CH):
         ip = np.asarray(ip, dtype=np.int64)
         G = check_split(ip, CH)
         M, nnz = len(ip) - 1, int(ip[-1])
-        assert G == (0 if M == 0 else max(1, -(-nnz // CH))), name
+        assert G == (0 if M == 0 else nnz // CH + 1), name
+        for view, n in _views(ip, CH):
+            check_split(view, CH, nnz=n)
 
 
 @pytest.mark.parametrize("seed", range(12))
@@ -141,6 +188,9 @@ def test_random_skew(seed):
     lengths[rng.random(M) < 0.2] = 0
     CH = int(rng.choice([3, 16, 64, 256, 512]))
     check_split(_indptr(lengths), CH)
+    for view, n in _views(_indptr(lengths), CH):
+        check_split(view, CH, nnz=n)
+        check_split(view, CH, cap=3, nnz=n)
 
 
 def test_scratch_edge_sends_long_rows_whole():
@@ -148,7 +198,7 @@ def test_scratch_edge_sends_long_rows_whole():
     summed whole by their first range and rows inside it are combined."""
     CH = 8
     ip = _indptr([3, 20, 2, 30, 0, 41, 5])
-    writes, pieces, whole, _G = stream_split(ip, CH, cap=4)
+    writes, pieces, whole, _G, _st = stream_split(ip, CH, cap=4)
     assert pieces[1] and not whole[1]          # nonzeros 3..22: ranges 0..2
     assert whole[3] == 1 and not pieces[3]     # nonzeros 25..54: ranges 3..6
     assert whole[5] == 1                       # nonzeros 55..95
@@ -170,9 +220,14 @@ def test_emitted_geometry_matches_the_model():
     g = generate(standard_kernels()["spmv"], cfg, "hip", write=False)
     geo = g.geometry
     assert geo.stream and geo.nnz_chunk == 512
-    assert (geo.grid(0, 0), geo.grid(5, 0), geo.grid(5, 512), geo.grid(5, 513)) == (0, 1, 1, 2)
-    assert "p0 = e * 512" in g.source
-    assert "(nnz + 512 - 1) / 512 : 1) : 0" in g.host_source
+    assert (geo.grid(0, 0), geo.grid(5, 0), geo.grid(5, 511), geo.grid(5, 512),
+            geo.grid(5, 513)) == (0, 1, 1, 2, 2)
+    assert "pa = pal + e * 512" in g.source
+    assert "const tg_i64 pbase = tg_uniform(s_b[6]), pend = tg_uniform(s_b[7]);" in g.source
+    # phase 1 runs first on the launch's own numbers, then again where they were wrong
+    assert "const tg_i64 pa = e * 512, sb = 0, se = nnz;" in g.source
+    assert "if (pbase != 0 || pend != nnz) {" in g.source
+    assert "rows > 0 ? (nnz > 0 ? nnz : 0) / 512 + 1 : 0" in g.host_source
     assert "tg_launch_ordered" in g.host_source      # module scratch: ordered launches
     odd = generate(standard_kernels()["spmv"],
                    Config(tile_size=64, threads_per_row=64, unroll=3, block_size=1024,

@@ -188,10 +188,12 @@ def _lowering(kernel: Kernel) -> Lowering:
 @dataclass
 class LaunchGeometry:
     """Grid rule of a HIP variant: ``grid = ceil(rows / rows_per_block)``,
-    plus ``ceil(nnz / nnz_chunk)`` workgroups ahead of those when
+    plus ``floor(nnz / nnz_chunk) + 1`` workgroups ahead of those when
     ``nnz_chunk`` is set (hybrid tiles' long-row workgroups).  With
-    ``stream`` the grid is ``ceil(nnz / nnz_chunk)`` alone, at least one
-    workgroup when there are rows (they are written even without nonzeros)."""
+    ``stream`` the grid is ``floor(nnz / nnz_chunk) + 1`` alone when there
+    are rows (they are written even without nonzeros).  Ranges are counted
+    from the even position at or below indptr[0], so nnz nonzeros meet at most
+    floor(nnz / nnz_chunk) + 1 of them."""
 
     rows_per_block: int
     block: int
@@ -204,10 +206,10 @@ class LaunchGeometry:
         if rows <= 0:
             return 0
         if self.stream:
-            return max(1, (int(nnz) + self.nnz_chunk - 1) // self.nnz_chunk)
+            return max(0, int(nnz)) // self.nnz_chunk + 1
         g = (int(rows) + self.rows_per_block - 1) // self.rows_per_block
-        if self.nnz_chunk and nnz > 0:
-            g += (int(nnz) + self.nnz_chunk - 1) // self.nnz_chunk
+        if self.nnz_chunk:
+            g += max(0, int(nnz)) // self.nnz_chunk + 1
         return g
 
     def to_dict(self) -> Dict[str, Any]:
@@ -845,13 +847,14 @@ __device__ __forceinline__ tg_i64 tg_mp_probe(tg_i64 g, int l) {
   return g + 24 + ((tg_i64)32 << (2 * (l - 56)));
 }
 
-// Smallest r in [0, R] with r + indptr[r] >= t (R when there is none);
-// X = R + nnz.  Run by all 64 lanes of one wave, one row pointer per lane per
-// round; the ballot of the test gives the bracket's new ends (the first lane
-// that passes and the lane before it), read from those lanes.  Each later round
-// probes 64 evenly spaced rows of the bracket left, so the bracket shrinks at
-// least 63-fold per round.
-__device__ tg_i64 tg_mp_search(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 t, tg_i64 X) {
+// Smallest r in [0, R] with r + indptr[r] - base >= t (R when there is none);
+// base = indptr[0], X = R + indptr[R] - base, the launch's items.  Run by all
+// 64 lanes of one wave, one row pointer per lane per round; the ballot of the
+// test gives the bracket's new ends (the first lane that passes and the lane
+// before it), read from those lanes.  Each later round probes 64 evenly spaced
+// rows of the bracket left, so the bracket shrinks at least 63-fold per round.
+__device__ tg_i64 tg_mp_search(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 t, tg_i64 X,
+                               tg_i64 base) {
   const int l = threadIdx.x & 63;
   const tg_i64 g = X > 0 ? (tg_i64)((double)t * ((double)R / (double)X)) : 0;
   tg_i64 q = tg_mp_probe(g, l);
@@ -859,7 +862,7 @@ __device__ tg_i64 tg_mp_search(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i
   #pragma unroll 1
   for (;;) {
     q = q < lo ? lo : (q > hi ? hi : q);
-    const unsigned long long m = __ballot(q + indptr[q] >= t);
+    const unsigned long long m = __ballot(q + indptr[q] - base >= t);
     const int f = m ? (int)__builtin_ctzll(m) : 64;   // first lane that passes
     const tg_i64 b = f < 64 ? tg_lane_read(q, f) : hi;
     const tg_i64 a = f > 0 ? tg_lane_read(q, f - 1) : lo - 1;   // rows before t
@@ -870,16 +873,16 @@ __device__ tg_i64 tg_mp_search(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i
   }
 }
 
-// The row holding nonzero position P, 0 <= P < X = indptr[R]: the one row r with
-// indptr[r] <= P < indptr[r + 1], returned with those two bounds in *rs and
-// *re.  Run by all 64 lanes of one wave, with the probes of tg_mp_search; the
-// bracket [lo, hi] keeps indptr[lo] <= P < indptr[hi] and carries both values,
-// so the bounds cost no load of their own.
-__device__ tg_i64 tg_mp_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 P, tg_i64 X,
-                            tg_i64* rs, tg_i64* re) {
+// The row holding nonzero position P, pb <= P < pe, where pb = indptr[0] and
+// pe = indptr[R]: the one row r with indptr[r] <= P < indptr[r + 1], returned
+// with those two bounds in *rs and *re.  Run by all 64 lanes of one wave, with
+// the probes of tg_mp_search; the bracket [lo, hi] keeps indptr[lo] <= P <
+// indptr[hi] and carries both values, so the bounds cost no load of their own.
+__device__ tg_i64 tg_mp_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 P, tg_i64 pb,
+                            tg_i64 pe, tg_i64* rs, tg_i64* re) {
   const int l = threadIdx.x & 63;
-  tg_i64 q = tg_mp_probe((tg_i64)((double)P * ((double)R / (double)X)), l);
-  tg_i64 lo = 0, hi = R, vlo = 0, vhi = X;   // indptr[0] = 0, indptr[R] = X
+  tg_i64 q = tg_mp_probe((tg_i64)((double)(P - pb) * ((double)R / (double)(pe - pb))), l);
+  tg_i64 lo = 0, hi = R, vlo = pb, vhi = pe;   // indptr[0] = pb, indptr[R] = pe
   #pragma unroll 1
   for (;;) {
     q = q < lo ? lo : (q > hi ? hi : q);
@@ -988,39 +991,64 @@ __device__ bool tg_mp_commit(unsigned long long* __restrict__ part, tg_i64 w, tg
            "__device__ unsigned long long tg_mp_part[%d];" % (2 * MERGE_CAP))})
 
 
-def _merge_window(w: _W, TR: int, WAVES: int) -> None:
+def _merge_window(w: _W, TR: int, WAVES: int, plan: Plan) -> None:
     """This workgroup's merge-path window, its rows and its row pieces
-    (defines r0, r1, r_own, pc_in, pc_out, s_win, wdx, D, t0, t1)."""
-    w("// merge-path window of this workgroup: items [t0, t1) of row_lim + nnz")
+    (defines pbase, pend, r0, r1, r_own, pc_in, pc_out, s_win, wdx, D, t0, t1).
+    The window searches first run on the launch's own numbers, as if
+    indptr[0] = 0 and indptr[M] = nnz, so that they wait for no other load;
+    once the row pointers have arrived (after the barrier) a workgroup whose
+    guess was wrong searches again."""
+    w("// merge-path window of this workgroup: items [t0, t1) of the launch's row_lim +")
+    w("// pend - pbase (row r is items r + indptr[r] - pbase ... r + indptr[r + 1] - pbase)")
     w("__shared__ tg_i64 s_win[6];  // r0, r1, indptr[r0 - 1], indptr[r0], indptr[r1 - 1], indptr[r1]")
     w("const tg_i64 G = gridDim.x, wdx = blockIdx.x;")
-    w("const tg_i64 X = row_lim + nnz;")
-    w("const tg_i64 D = X > G ? (X + G - 1) / G : 1;  // items per window")
-    w("const tg_i64 t0 = wdx * D < X ? wdx * D : X;")
-    w("const tg_i64 t1 = t0 + D < X ? t0 + D : X;")
-    w("// first and last rows: the first row beginning at or after t0 (t1)")
-    w.open("if (threadIdx.x < 64)")
-    w("const tg_i64 a = wdx == 0 ? 0 : tg_mp_search(indptr, row_lim, t0, X);")
-    w("if (threadIdx.x == 0) s_win[0] = a;")
-    w("if (threadIdx.x < 2) s_win[2 + threadIdx.x] = a - 1 + (tg_i64)threadIdx.x >= 0 ? "
-      "indptr[a - 1 + threadIdx.x] : 0;")
-    w.close()
     sel = "threadIdx.x >= 64 && threadIdx.x < 128" if WAVES > 1 else "threadIdx.x < 64"
-    w.open("if (%s)" % sel)
-    w("const tg_i64 b = wdx == G - 1 ? row_lim : tg_mp_search(indptr, row_lim, t1, X);")
-    w("const int l = threadIdx.x & 63;")
-    w("if (l == 0) s_win[1] = b;")
-    w("if (l < 2) s_win[4 + l] = b - 1 + l >= 0 ? indptr[b - 1 + l] : 0;")
+
+    def searches(base: str) -> None:
+        w("// first and last rows: the first row beginning at or after t0 (t1)")
+        w.open("if (threadIdx.x < 64)")
+        w("const tg_i64 a = wdx == 0 ? 0 : tg_mp_search(indptr, row_lim, t0, X, %s);" % base)
+        w("if (threadIdx.x == 0) s_win[0] = a;")
+        w("if (threadIdx.x < 2) s_win[2 + threadIdx.x] = a - 1 + (tg_i64)threadIdx.x >= 0 ? "
+          "indptr[a - 1 + threadIdx.x] : 0;")
+        w.close()
+        w.open("if (%s)" % sel)
+        w("const tg_i64 b = wdx == G - 1 ? row_lim : tg_mp_search(indptr, row_lim, t1, X, %s);"
+          % base)
+        w("const int l = threadIdx.x & 63;")
+        w("if (l == 0) s_win[1] = b;")
+        w("if (l < 2) s_win[4 + l] = b - 1 + l >= 0 ? indptr[b - 1 + l] : 0;")
+        w.close()
+
+    def window(nz: str) -> None:
+        w("const tg_i64 X = row_lim + %s;" % nz)
+        w("const tg_i64 D = X > G ? (X + G - 1) / G : 1;  // items per window")
+        w("const tg_i64 t0 = wdx * D < X ? wdx * D : X;")
+        w("const tg_i64 t1 = t0 + D < X ? t0 + D : X;")
+
+    w("tg_i64 vpb, vpe;")
+    _positions(w, plan, declare=False)
+    w.open("")
+    window("(nnz > 0 ? nnz : 0)")
+    searches("0")
     w.close()
     w("__syncthreads();")
+    w("const tg_i64 pbase = tg_uniform(vpb), pend = tg_uniform(vpe);")
+    window("(pend - pbase)")
+    w.open("if (pbase != 0 || pend != nnz)")
+    w("// the guess was wrong (a block of rows of a larger matrix, or nnz other than the")
+    w("// rows' count): the searches again, on the row pointers' numbers")
+    searches("pbase")
+    w("__syncthreads();")
+    w.close()
     w("const tg_i64 r0 = s_win[0], r1 = s_win[1];")
     w("// a row longer than a window is cut at the window edges when every window it")
     w("// reaches has scratch slots (below %d); this window holds a piece of the row that" % MERGE_CAP)
     w("// began before it, if that row reaches into it, and of its own last row")
     w("const bool pc_in = r0 > 0 && s_win[3] - s_win[2] > D && "
-      "(r0 - 1 + s_win[3] - 1) / D < %d && r0 - 1 + s_win[3] > t0;" % MERGE_CAP)
+      "(r0 - 1 + s_win[3] - pbase - 1) / D < %d && r0 - 1 + s_win[3] - pbase > t0;" % MERGE_CAP)
     w("const bool pc_out = r1 > r0 && s_win[5] - s_win[4] > D && "
-      "(r1 - 1 + s_win[5] - 1) / D < %d;" % MERGE_CAP)
+      "(r1 - 1 + s_win[5] - pbase - 1) / D < %d;" % MERGE_CAP)
     w("const tg_i64 r_own = pc_out ? r1 - 1 : r1;  // rows summed whole, %d at a time" % TR)
 
 
@@ -1038,7 +1066,10 @@ def _value_row_free(plan: Plan) -> bool:
 def _hybrid_ranges(w: _W, plan: Plan, step, out_name: str, B: int, U: int, ALIGN: int,
                    WAVES: int, CH: int, LH: int) -> None:
     """The long-row workgroups of hybrid tiles (defines GL; those workgroups
-    return).  Workgroup e < GL takes nonzeros [p0, p1) = [e CH, (e+1) CH).
+    return).  Range e holds the positions [pa, pa + CH), pa = (pbase & ~1) + e CH,
+    clipped to [p0, p1) inside [pbase, pend); the GL range workgroups take every
+    GL-th range, GL from the launch's nnz, so the ranges (and the result) come
+    from the row pointers alone.
 
     A row longer than LH = CH / 2 that meets the range holds p0, p0 + LH or
     p1 - 1, so three waves (one each) find the rows holding those positions
@@ -1062,18 +1093,66 @@ def _hybrid_ranges(w: _W, plan: Plan, step, out_name: str, B: int, U: int, ALIGN
                          "value and the gathered operand")
     gathered = _gather_operand(plan)
     col = plan.col_idx.name
-    w("// workgroups below GL sum the rows longer than %d nonzeros, %d nonzeros each;" % (LH, CH))
-    w("// the rest are row tiles, which leave those rows alone")
-    w("const tg_i64 GL = nnz > 0 ? (nnz + %d) / %d : 0;" % (CH - 1, CH))
+    w("// workgroups below GL sum the rows longer than %d nonzeros, over ranges of %d;" % (LH, CH))
+    w("// the rest are row tiles, which leave those rows alone.  GL comes from the")
+    w("// launch's nnz (it sized the grid), the ranges from the row pointers: range e")
+    w("// holds the positions [pa, pa + %d) from the even anchor pal = pbase & ~1 (so" % CH)
+    w("// 128-bit pairs stay aligned), clipped to [p0, p1) inside [pbase, pend).  Only the")
+    w("// first NL = min(NR, GL) ranges exist: the last of them also sums what the row")
+    w("// holding its last position has past it, and a long row beginning past it stays")
+    w("// with its row tile (nothing of either when nnz covers the rows' nonzeros)")
+    w("const tg_i64 GL = (nnz > 0 ? nnz : 0) / %d + 1;" % CH)
     w.open("if ((tg_i64)blockIdx.x < GL)")
     w("__shared__ tg_i64 s_lr[9];  // the rows holding p0, p0 + LH, p1 - 1: row, start, end")
     w("__shared__ double s_hred[%d];  // [wave][listed row]" % (3 * WAVES))
     w("__shared__ double s_kred[%d];" % WAVES)
-    w("const tg_i64 e = blockIdx.x;")
-    w("const tg_i64 p0 = e * %d, p1 = p0 + %d < nnz ? p0 + %d : nnz;" % (CH, CH, CH))
     w("const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);")
+    w("const tg_i64 e = blockIdx.x;")
+
+    def searches(sb: str, se: str) -> None:
+        """Waves 0-2 find the rows holding the range's three probe positions
+        among the nonzeros [sb, se) and stage them in s_lr."""
+        w("// a row longer than %d that meets [p0, p1) holds p0, p0 + %d or p1 - 1 (one lying"
+          % (LH, LH))
+        w("// strictly inside the range is longer than half of it, so it holds the middle):")
+        w("// wave k finds the row holding the k-th of those positions, with its bounds")
+        w("#pragma unroll 1")
+        w.open("for (int k = wv; k < 3 && p0 < p1; k += %d)" % WAVES)
+        w("const tg_i64 P = k == 0 ? p0 : (k == 1 && p0 + %d < p1 ? p0 + %d : p1 - 1);" % (LH, LH))
+        w("tg_i64 rs, re;")
+        w("const tg_i64 r = tg_mp_row(indptr, row_end, P, %s, %s, &rs, &re);" % (sb, se))
+        w("if ((threadIdx.x & 63) == 0) { s_lr[3 * k] = r; s_lr[3 * k + 1] = rs; "
+          "s_lr[3 * k + 2] = re; }")
+        w.close()
+
+    w("// The searches first run on the launch's own numbers, as if indptr[0] = 0 and")
+    w("// indptr[M] = nnz (the common case), so that they wait for no other load; the")
+    w("// guess is checked once the row pointers have arrived, after the barrier.")
+    w("tg_i64 vpb, vpe;")
+    _positions(w, plan, declare=False)
+    w.open("")
+    w("const tg_i64 p0 = e * %d, p1 = p0 + %d < nnz ? p0 + %d : (nnz > p0 ? nnz : p0);"
+      % (CH, CH, CH))
+    searches("0", "nnz")
+    w.close()
+    w("__syncthreads();")
+    w("const tg_i64 pbase = tg_uniform(vpb), pend = tg_uniform(vpe);")
+    w("const tg_i64 pal = pbase & ~(tg_i64)1;")
+    w("const tg_i64 NR = pend > pbase ? (pend - pal + %d) / %d : 0;" % (CH - 1, CH))
+    w("const tg_i64 NL = NR < GL ? NR : GL;")
+    w("if (e >= NL) return;")
+    w("const bool last = e == NL - 1;")
+    w("const tg_i64 pa = pal + e * %d;" % CH)
+    w("const tg_i64 p0 = pa > pbase ? pa : pbase, p1 = pa + %d < pend ? pa + %d : pend;"
+      % (CH, CH))
+    w.open("if (pbase != 0 || pend != nnz)")
+    w("// the guess was wrong (a block of rows of a larger matrix, or nnz other than the")
+    w("// rows' count): the searches again, on the row pointers' numbers")
+    searches("pbase", "pend")
+    w("__syncthreads();")
+    w.close()
     def load_range(sel: Callable[[int, str], str]) -> None:
-        """Indices and values of lane l's positions p0 + s B U + l U + u in hi_/hv_,
+        """Indices and values of lane l's positions pa + s B U + l U + u in hi_/hv_,
         with every load issued unconditionally (a load under a lane-varying branch
         is waited for before the branch joins).  ``sel(s, q)`` is the lane's
         condition to load its own positions; other lanes load the range's first
@@ -1081,10 +1160,10 @@ def _hybrid_ranges(w: _W, plan: Plan, step, out_name: str, B: int, U: int, ALIGN
         w("tg_i64 hi_[%d]; double hv_[%d];" % (NS * U, NS * U))
         for s_ in range(NS):
             q = "qs%d" % s_
-            w("const tg_i64 %s = p0 + %d + (tg_i64)threadIdx.x * %d;" % (q, s_ * B * U, U))
+            w("const tg_i64 %s = pa + %d + (tg_i64)threadIdx.x * %d;" % (q, s_ * B * U, U))
             w("const tg_i64 qe%d = %s ? %s : p0;" % (s_, sel(s_, q), q))
         if U % 2 == 0:
-            w("// whole range, 16-byte aligned bases: 128-bit pairs for every lane")
+            w("// whole range (so p0 = pa, even), 16-byte aligned bases: 128-bit pairs")
             w.open("if (pair_ok && p1 - p0 == %d)" % CH)
             for s_ in range(NS):
                 for u in range(0, U, 2):
@@ -1097,26 +1176,16 @@ def _hybrid_ranges(w: _W, plan: Plan, step, out_name: str, B: int, U: int, ALIGN
             w.open("else")
         else:
             w.open("")
-        w("// the last range, or bases only 8-byte aligned: per element, clamped into the arrays")
+        w("// a clipped range, or bases only 8-byte aligned: per element, clamped into [p0, p1)")
         for s_ in range(NS):
             for u in range(U):
                 o = s_ * U + u
-                w("{ const tg_i64 c = qe%d + %d < nnz ? qe%d + %d : nnz - 1;"
+                w("{ const tg_i64 c = qe%d + %d < p1 ? (qe%d + %d >= p0 ? qe%d + %d : p0) : p1 - 1;"
                   " hi_[%d] = __builtin_nontemporal_load(indices + c);"
-                  " hv_[%d] = __builtin_nontemporal_load(data + c); }" % (s_, u, s_, u, o, o))
+                  " hv_[%d] = __builtin_nontemporal_load(data + c); }"
+                  % (s_, u, s_, u, s_, u, o, o))
         w.close()
 
-    w("// a row longer than %d that meets [p0, p1) holds p0, p0 + %d or p1 - 1 (one lying" % (LH, LH))
-    w("// strictly inside the range is longer than half of it, so it holds the middle):")
-    w("// wave k finds the row holding the k-th of those positions, with its bounds")
-    w("#pragma unroll 1")
-    w.open("for (int k = wv; k < 3; k += %d)" % WAVES)
-    w("const tg_i64 P = k == 0 ? p0 : (k == 1 && p0 + %d < p1 ? p0 + %d : p1 - 1);" % (LH, LH))
-    w("tg_i64 rs, re;")
-    w("const tg_i64 r = tg_mp_row(indptr, row_end, P, nnz, &rs, &re);")
-    w("if ((threadIdx.x & 63) == 0) { s_lr[3 * k] = r; s_lr[3 * k + 1] = rs; s_lr[3 * k + 2] = re; }")
-    w.close()
-    w("__syncthreads();")
     w("// the distinct long rows among them (the positions ascend, so a row found twice is")
     w("// found by neighbouring waves)")
     w("tg_i64 kr[3], ks[3], ke[3];")
@@ -1151,7 +1220,7 @@ def _hybrid_ranges(w: _W, plan: Plan, step, out_name: str, B: int, U: int, ALIGN
     w("double part[3] = {0.0, 0.0, 0.0};")
     w("#pragma unroll")
     w.open("for (int i = 0; i < %d; ++i)" % (NS * U))
-    w("const tg_i64 pu = p0 + (i / %d) * %d + (tg_i64)threadIdx.x * %d + i %% %d;"
+    w("const tg_i64 pu = pa + (i / %d) * %d + (tg_i64)threadIdx.x * %d + i %% %d;"
       % (U, B * U, U, U))
     w("const double pv = mk_[i] ? %s : 0.0;" % _value_with(plan, "hv_[i]", "xg_[i]", "0", "hi_[i]"))
     w("#pragma unroll")
@@ -1171,13 +1240,25 @@ def _hybrid_ranges(w: _W, plan: Plan, step, out_name: str, B: int, U: int, ALIGN
     w.open("for (int k = wv; k < 3; k += %d)" % WAVES)
     w("const tg_i64 r = s_lr[3 * k], rs = s_lr[3 * k + 1], re = s_lr[3 * k + 2];")
     w("if (!(re - rs > %d && (k == 0 || r != s_lr[3 * k - 3]))) continue;" % LH)
-    w("const tg_i64 ef = rs / %d, el = (re - 1) / %d;  // the ranges its nonzeros lie in"
-      % (CH, CH))
+    w("// the ranges it spans (ranges past the grid's last do not exist)")
+    w("const tg_i64 ef = (rs - pal) / %d, el0 = (re - 1 - pal) / %d;" % (CH, CH))
+    w("const tg_i64 el = el0 < NL - 1 ? el0 : NL - 1;")
     w("const bool cut = el > ef && el < %d;" % MERGE_CAP)
     w("if (!cut && el != ef) continue;  // kept whole: summed by its first range below")
     w("double t = 0.0;")
     w("#pragma unroll")
     w("for (int v = 0; v < %d; ++v) t += s_hred[3 * v + k];" % WAVES)
+    w.open("if (last && re > p1)")
+    w("// the grid's last range: this row's positions past the range, with its own loads")
+    w("double tt = 0.0;")
+    w("#pragma unroll 1")
+    w.open("for (tg_i64 pq = p1 + (threadIdx.x & 63); pq < re; pq += 64)")
+    w("const tg_i64 cq = indices[pq];")
+    w("tt += %s;" % _value_with(plan, "data[pq]", _cexpr(gathered, _Env({row: "r", col: "cq"},
+                                                                       p="pq")), "r", "cq"))
+    w.close()
+    w("t += tg_segsum<64>(tt);")
+    w.close()
     w("double tot = t;")
     w("const bool done = !cut || tg_mp_commit(tg_part, e, ef, el, t, &tot);")
     w.open("if (done && (threadIdx.x & 63) == 0)")
@@ -1192,12 +1273,13 @@ def _hybrid_ranges(w: _W, plan: Plan, step, out_name: str, B: int, U: int, ALIGN
     w.open("for (int k = 0; k < 3; ++k)")
     w("const tg_i64 row = s_lr[3 * k], rs = s_lr[3 * k + 1], re = s_lr[3 * k + 2];")
     w("if (!(re - rs > %d && (k == 0 || row != s_lr[3 * k - 3]))) continue;" % LH)
-    w("if (rs / %d != e || (re - 1) / %d < %d) continue;" % (CH, CH, MERGE_CAP))
+    w("if ((rs - pal) / %d != e || ((re - 1 - pal) / %d < NL - 1 ? (re - 1 - pal) / %d : NL - 1) "
+      "< %d) continue;" % (CH, CH, CH, MERGE_CAP))
     w("double cacc = 0.0;")
     w("#pragma unroll 1")
     w.open("for (tg_i64 q = (rs & ~(tg_i64)%d) + (tg_i64)threadIdx.x * %d; q < re; q += %d)"
            % (ALIGN - 1, U, B * U))
-    step("q", "rs", "re", "cacc")
+    step("q", "rs", "re", "cacc", "rs", "re")
     w.close()
     w("cacc = tg_segsum<64>(cacc);")
     w("if ((threadIdx.x & 63) == 0) s_kred[wv] = cacc;")
@@ -1216,17 +1298,49 @@ def _hybrid_ranges(w: _W, plan: Plan, step, out_name: str, B: int, U: int, ALIGN
     w.close()
 
 
+def _positions(w: _W, plan: Plan, declare: bool = True) -> None:
+    """vpb / vpe: indptr[0] and indptr[M], the first and one-past-last nonzero
+    positions of the rows (pbase, pend once read with tg_uniform).  indptr[0]
+    may be nonzero: a block of rows of a larger matrix whose indices/data are
+    passed whole, as the reference's kernels allow (they walk rows by indptr
+    alone and never read nnz).
+
+    They are vector loads, made relaxed atomic so that the compiler neither
+    moves them down to their first use nor waits right after them.  Vector
+    loads return in order, so a caller issues them just after the loads its
+    next wait is for: that wait then covers them at no cost, and no earlier
+    wait includes them."""
+    w("// indptr[0] and indptr[M] as vector loads (relaxed atomic: issued here, not moved")
+    w("// down to their first use, and not waited for at once)")
+    if declare:
+        w("tg_i64 vpb, vpe;")
+    w.open("")
+    w("// a global (not flat) pointer: flat loads also count as LDS accesses, so any wait")
+    w("// for an LDS access or a scalar load would wait for them too")
+    w("typedef const __attribute__((address_space(1))) tg_i64 tg_gi64;")
+    w("tg_gi64* ip_ = (tg_gi64*)indptr;")
+    w('asm volatile("" : "+v"(ip_));')
+    w("vpb = __hip_atomic_load(ip_, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);")
+    w("vpe = __hip_atomic_load(ip_ + %s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);"
+      % plan.row_extent)
+    w.close()
+
+
 def _hip_stream_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeometry,
                        out_name: str, pre: _W, scratch_arg: bool = False) -> None:
     """y[row] = final(sum over the row's nonzeros of value_expr), one equal range of
     nonzeros per workgroup (``balance == "stream"``).
 
-    Workgroup e takes the nonzeros [p0, p1) = [e CH, (e+1) CH), CH = B U, and
+    Range e takes the nonzero positions [p0, p1): the CH = B U positions from
+    pa = (pbase & ~1) + e CH, clipped to [pbase, pend) = [indptr[0], indptr[M])
+    (the even anchor keeps 128-bit pairs aligned when indptr[0] is odd), and
     owns the rows [ra, rb): ra is the row holding p0 (0 for e = 0, so the first
-    workgroup also owns the empty rows ahead of the first nonzero) and rb the
-    row holding p1 (M for the last workgroup).  Every row belongs to exactly one
-    workgroup: the one its last nonzero lies in (for an empty row, the one its
-    position lies in).
+    range also owns the empty rows ahead of the first nonzero) and rb the row
+    holding p1 (M for the last range).  Every row belongs to exactly one range:
+    the one its last nonzero lies in (for an empty row, the one its position
+    lies in).  The ranges come from the row pointers; workgroup g takes ranges
+    g, g + G, ... (G = the grid, sized from nnz), so the launch's nnz changes
+    the grid and never the result.
 
     1. Every lane loads its U nonzeros (128-bit (index, value) pairs, coalesced
        over the workgroup), then waves 0 and 1 find ra and rb with
@@ -1275,17 +1389,28 @@ def _hip_stream_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("__builtin_nontemporal_store(%s, %s + %s);" % (
             _cexpr(plan.final_expr, env), out_name, _offset(plan.out_tensor, plan.out.indices, env)))
 
+    def tail(lo: str, hi: str, acc: str) -> None:
+        """One wave adds the row's positions [lo, hi) past the staged ones, with its
+        own loads (only the grid's last range, when nnz undercounts the rows'
+        nonzeros, has any)."""
+        w("#pragma unroll 1")
+        w.open("for (tg_i64 pq = (%s) + l; pq < (%s); pq += 64)" % (lo, hi))
+        w("const tg_i64 cq = indices[pq];")
+        w("%s += %s;" % (acc, _value_with(plan, "data[pq]", gather("cq"), row, "cq")))
+        w.close()
+
     _merge_decls(pre, scratch_arg)
-    pre(r"""// The row holding nonzero position P, 0 <= P < X = indptr[R], with its bounds in *rs
-// and *re: tg_mp_row's contract and later rounds, with a first round for skewed rows.
-// It probes every 64th row across 2048 rows either side of the proportional guess, so
-// a row that close is found in two rounds (the second probes its bracket row by row);
-// the rows of a power-law or dense-row matrix lie within that distance of the guess.
-__device__ tg_i64 tg_st_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 P, tg_i64 X,
-                            tg_i64* rs, tg_i64* re) {
+    pre(r"""// The row holding nonzero position P, pb <= P < pe (pb = indptr[0], pe = indptr[R]),
+// with its bounds in *rs and *re: tg_mp_row's contract and later rounds, with a first
+// round for skewed rows.  It probes every 64th row across 2048 rows either side of the
+// proportional guess, so a row that close is found in two rounds (the second probes its
+// bracket row by row); the rows of a power-law or dense-row matrix lie within that
+// distance of the guess.
+__device__ tg_i64 tg_st_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 P, tg_i64 pb,
+                            tg_i64 pe, tg_i64* rs, tg_i64* re) {
   const int l = threadIdx.x & 63;
-  tg_i64 q = (tg_i64)((double)P * ((double)R / (double)X)) + (tg_i64)(l - 32) * 64;
-  tg_i64 lo = 0, hi = R, vlo = 0, vhi = X;   // indptr[0] = 0, indptr[R] = X
+  tg_i64 q = (tg_i64)((double)(P - pb) * ((double)R / (double)(pe - pb))) + (tg_i64)(l - 32) * 64;
+  tg_i64 lo = 0, hi = R, vlo = pb, vhi = pe;   // indptr[0] = pb, indptr[R] = pe
   #pragma unroll 1
   for (;;) {
     q = q < lo ? lo : (q > hi ? hi : q);
@@ -1309,76 +1434,134 @@ __device__ tg_i64 tg_st_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 
     w("const tg_i64 n_rows = %s;  // rows of the matrix" % plan.row_extent)
     w("__shared__ double s_prod[%d];  // this range's products" % CH)
     w("__shared__ tg_i64 s_ptr[%d];  // owned rows' pointers, %d rows at a time" % (RB + 1, RB))
-    w("__shared__ tg_i64 s_b[6];  // the rows holding p0 and p1: row, start, end")
+    w("__shared__ tg_i64 s_b[8];  // the rows holding p0 and p1: row, start, end; indptr[0], indptr[M]")
     w("__shared__ int s_long[%d];  // staged rows over 64 nonzeros" % RB)
     w("__shared__ int s_nlong;")
     w("__shared__ double s_wsum[%d];  // the waves' sums of a row past the scratch" % WAVES)
     w("const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);")
     w("const int l = threadIdx.x & 63;")
-    w("const tg_i64 e = blockIdx.x;")
-    w("const tg_i64 p0 = e * %d, p1 = p0 + %d < nnz ? p0 + %d : nnz;" % (CH, CH, CH))
-    w("const int cnt = (int)(p1 - p0);  // nonzeros in this range")
-    w("// 1. this range's indices and values, every load issued before any is used")
-    w("tg_i64 ci[%d]; double cv[%d];" % (U, U))
+    w("tg_i64 vpb, vpe;  // indptr[0] and indptr[M], loaded during phase 1")
     if U % 2 == 0:
         w("// 128-bit (index, value) pair loads need 16-byte aligned bases; a caller's")
         w("// sub-buffer may be only 8-byte aligned, which takes the per-element loads")
         w("const bool pair_ok = ((((unsigned long long)indices) | "
           "((unsigned long long)data)) & 15) == 0;")
-        for u in range(0, U, 2):
-            w.open("")
-            w("const int q = %s;" % pos(u))
-            w.open("if (pair_ok && q + 1 < cnt)")
-            w("const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + p0 + q));")
-            w("const tg_f64x2 b = __builtin_nontemporal_load((const tg_f64x2*)(data + p0 + q));")
-            w("ci[%d] = a.x; ci[%d] = a.y; cv[%d] = b.x; cv[%d] = b.y;" % (u, u + 1, u, u + 1))
+    w("const tg_i64 e = blockIdx.x;")
+
+    def phase1(positions: bool) -> None:
+        """Stage the range's products and find its bounding rows, for positions
+        pa + q, q in [qlo, qhi), and the rows holding P0 and P1 among the
+        nonzeros [sb, se); with ``positions``, also load indptr[0] and
+        indptr[M] once the range's own loads are issued."""
+        w("// 1. this range's indices and values, every load issued before any is used")
+        w("tg_i64 ci[%d]; double cv[%d];" % (U, U))
+        if U % 2 == 0:
+            for u in range(0, U, 2):
+                w.open("")
+                w("const int q = %s;" % pos(u))
+                w.open("if (pair_ok && q >= qlo && q + 1 < qhi)")
+                w("const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + pa + q));")
+                w("const tg_f64x2 b = __builtin_nontemporal_load((const tg_f64x2*)(data + pa + q));")
+                w("ci[%d] = a.x; ci[%d] = a.y; cv[%d] = b.x; cv[%d] = b.y;" % (u, u + 1, u, u + 1))
+                w.close()
+                w.open("else")
+                for d in (0, 1):
+                    w("ci[%d] = ((q + %d >= qlo) & (q + %d < qhi)) ? "
+                      "__builtin_nontemporal_load(indices + pa + q + %d) : 0;" % (u + d, d, d, d))
+                    w("cv[%d] = ((q + %d >= qlo) & (q + %d < qhi)) ? "
+                      "__builtin_nontemporal_load(data + pa + q + %d) : 0.0;" % (u + d, d, d, d))
+                w.close()
+                w.close()
+        else:
+            for u in range(U):
+                w.open("")
+                w("const int q = %s;" % pos(u))
+                w("ci[%d] = ((q >= qlo) & (q < qhi)) ? __builtin_nontemporal_load(indices + pa + q) : 0;"
+                  % u)
+                w("cv[%d] = ((q >= qlo) & (q < qhi)) ? __builtin_nontemporal_load(data + pa + q) : 0.0;"
+                  % u)
+                w.close()
+        if positions:
+            w("// wave 0 alone loads indptr[0] and indptr[M] (for the check after the barrier)")
+            w.open("if (wv == 0)")
+            _positions(w, plan, declare=False)
             w.close()
-            w.open("else")
-            for d in (0, 1):
-                w("ci[%d] = q + %d < cnt ? __builtin_nontemporal_load(indices + p0 + q + %d) : 0;"
-                  % (u + d, d, d))
-                w("cv[%d] = q + %d < cnt ? __builtin_nontemporal_load(data + p0 + q + %d) : 0.0;"
-                  % (u + d, d, d))
-            w.close()
-            w.close()
-    else:
+        w("if (threadIdx.x == 0) s_nlong = 0;")
+        w("// the rows holding P0 (wave 0) and P1 (wave 1), searched while the loads are in")
+        w("// flight; the first range owns the rows from 0, the last the rows up to M")
+        w("#pragma unroll 1")
+        w.open("for (int k = wv; k < 2; k += %d)" % WAVES)
+        w("const tg_i64 P = k == 0 ? P0 : P1;")
+        w("tg_i64 r = n_rows, rs = se, re = se;")
+        w("if (k == 0 && e == 0) { r = 0; rs = sb; re = sb; }")
+        w("else if (P < se) r = tg_st_row(indptr, n_rows, P, sb, se, &rs, &re);")
+        w("if (l == 0) { s_b[3 * k] = r; s_b[3 * k + 1] = rs; s_b[3 * k + 2] = re; }")
+        w.close()
+        if positions:
+            w("if (threadIdx.x == 0) { s_b[6] = vpb; s_b[7] = vpe; }")
+        w("// the operands (positions past the range gather nothing) and the products, in LDS")
+        w("double xv[%d];" % U)
         for u in range(U):
-            w.open("")
-            w("const int q = %s;" % pos(u))
-            w("ci[%d] = q < cnt ? __builtin_nontemporal_load(indices + p0 + q) : 0;" % u)
-            w("cv[%d] = q < cnt ? __builtin_nontemporal_load(data + p0 + q) : 0.0;" % u)
-            w.close()
-    w("if (threadIdx.x == 0) s_nlong = 0;")
-    w("// the rows holding p0 (wave 0) and p1 (wave 1), searched while the loads are in")
-    w("// flight; the first range owns the rows from 0, the last the rows up to M")
-    w("#pragma unroll 1")
-    w.open("for (int k = wv; k < 2; k += %d)" % WAVES)
-    w("const tg_i64 P = k == 0 ? p0 : p1;")
-    w("tg_i64 r = n_rows, rs = nnz, re = nnz;")
-    w("if (k == 0 && e == 0) { r = 0; rs = 0; re = 0; }")
-    w("else if (P < nnz) r = tg_st_row(indptr, n_rows, P, nnz, &rs, &re);")
-    w("if (l == 0) { s_b[3 * k] = r; s_b[3 * k + 1] = rs; s_b[3 * k + 2] = re; }")
+            w("{ const int q = %s; xv[%d] = ((q >= qlo) & (q < qhi)) ? %s : 0.0; }"
+              % (pos(u), u, gather("ci[%d]" % u)))
+        for u in range(U):
+            w("{ const int q = %s; if ((q >= qlo) & (q < qhi)) s_prod[q] = %s; }"
+              % (pos(u), _value_with(plan, "cv[%d]" % u, "xv[%d]" % u, row, "ci[%d]" % u)))
+
+    w("// Phase 1 first runs on the launch's own numbers, as if indptr[0] = 0 and")
+    w("// indptr[M] = nnz (the common case), so that its loads wait for nothing: range e")
+    w("// stages the positions [e %d, (e + 1) %d) below nnz.  Once the row pointers have" % (CH, CH))
+    w("// arrived (after the barrier) the guess is checked, and a workgroup whose guess")
+    w("// was wrong runs phase 1 again on the row pointers' numbers (below).")
+    w.open("")
+    w("const tg_i64 pa = e * %d, sb = 0, se = nnz;" % CH)
+    w("const int qlo = 0, qhi = (int)(nnz > pa ? (nnz - pa < %d ? nnz - pa : %d) : 0);" % (CH, CH))
+    w("const tg_i64 P0 = pa, P1 = pa + qhi;")
+    phase1(True)
     w.close()
-    w("// the operands (positions past the range gather nothing) and the products, in LDS")
-    w("double xv[%d];" % U)
-    for u in range(U):
-        w("{ const int q = %s; xv[%d] = q < cnt ? %s : 0.0; }" % (pos(u), u, gather("ci[%d]" % u)))
-    for u in range(U):
-        w("{ const int q = %s; if (q < cnt) s_prod[q] = %s; }"
-          % (pos(u), _value_with(plan, "cv[%d]" % u, "xv[%d]" % u, row, "ci[%d]" % u)))
     w("__syncthreads();")
+    w("const tg_i64 pbase = tg_uniform(s_b[6]), pend = tg_uniform(s_b[7]);")
+    w("// range e stages the positions [pa, pa + %d), pa = pal + e * %d from the even"
+      % (CH, CH))
+    w("// anchor pal = pbase & ~1 (so 128-bit pairs stay aligned), clipped to [p0, ps) inside")
+    w("// [pbase, pend); a matrix without nonzeros still has one range, which writes its")
+    w("// empty rows.  The ranges come from the row pointers and the grid from nnz: only")
+    w("// the first NL = min(NR, grid) ranges exist, and the last of them owns every row up")
+    w("// to M, summing what lies past its staged positions with its own loads (nothing")
+    w("// when nnz covers the rows' nonzeros), so nnz never changes the product")
+    w("const tg_i64 pal = pbase & ~(tg_i64)1;")
+    w("const tg_i64 NR = pend > pbase ? (pend - pal + %d) / %d : 1;" % (CH - 1, CH))
+    w("const tg_i64 NL = NR < (tg_i64)gridDim.x ? NR : (tg_i64)gridDim.x;")
+    w("if (e >= NL) return;")
+    w("const bool last = e == NL - 1;")
+    w("const tg_i64 pa = pal + e * %d;" % CH)
+    w("const tg_i64 p0 = pa > pbase ? pa : pbase;")
+    w("const tg_i64 ps = pa + %d < pend ? pa + %d : pend;  // end of the staged positions"
+      % (CH, CH))
+    w("const tg_i64 p1 = last ? pend : ps;  // end of the positions this range owns")
+    w("// staged positions pa + q, q in [qlo, qhi)")
+    w("const int qlo = (int)(p0 - pa), qhi = (int)(ps - pa);")
+    w.open("if (pbase != 0 || pend != nnz)")
+    w("// the guess was wrong (a block of rows of a larger matrix, or nnz other than the")
+    w("// rows' count): phase 1 again, on the row pointers' numbers")
+    w("const tg_i64 sb = pbase, se = pend, P0 = p0, P1 = p1;")
+    phase1(False)
+    w("__syncthreads();")
+    w.close()
     w("const tg_i64 ra = s_b[0], ra_s = s_b[1], ra_e = s_b[2];")
     w("const tg_i64 rb = s_b[3], rb_s = s_b[4], rb_e = s_b[5];")
     w("// row ra began in an earlier range, so this range holds its last piece")
     w("const bool ra_cut = e > 0 && ra < rb && ra_s < p0;")
     w("// 2. the pieces cut at range edges first, so that their atomics overlap the row sums")
     w.open("if (wv == 0 && ra_cut)")
-    w("const tg_i64 ef = ra_s / %d, el = (ra_e - 1) / %d;  // the ranges it spans" % (CH, CH))
+    w("// the ranges it spans (ra ends in this range: it holds p0 and ends before rb)")
+    w("const tg_i64 ef = (ra_s - pal) / %d, el = e;" % CH)
     w.open("if (el < %d)" % MERGE_CAP)
-    w("const int en = (int)(ra_e - p0);")
+    w("const int en = (int)(ra_e - pa);")
     w("double t = 0.0;")
     w("#pragma unroll 4")
-    w("for (int q = l; q < en; q += 64) t += s_prod[q];")
+    w("for (int q = qlo + l; q < (en < qhi ? en : qhi); q += 64) t += s_prod[q];")
+    tail("ps > ra_s ? ps : ra_s", "ra_e", "t")
     w("t = tg_segsum<64>(t);")
     w("double tot = t;")
     w.open("if (tg_mp_commit(tg_part, e, ef, el, t, &tot) && l == 0 && ra < row_end)")
@@ -1388,12 +1571,13 @@ __device__ tg_i64 tg_st_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 
     w("// otherwise the range it begins in sums it whole (below)")
     w.close()
     w.open("if (wv == %d && rb < n_rows && rb_s < p1)" % (1 if WAVES > 1 else 0))
-    w("const tg_i64 ef = rb_s / %d, el = (rb_e - 1) / %d;" % (CH, CH))
+    w("const tg_i64 ef = (rb_s - pal) / %d, el0 = (rb_e - 1 - pal) / %d;" % (CH, CH))
+    w("const tg_i64 el = el0 < NL - 1 ? el0 : NL - 1;  // ranges past the grid's last do not exist")
     w.open("if (el < %d)" % MERGE_CAP)
-    w("const int st = (int)((rb_s > p0 ? rb_s : p0) - p0);")
+    w("const int st = (int)((rb_s > p0 ? rb_s : p0) - pa);")
     w("double t = 0.0;")
     w("#pragma unroll 4")
-    w("for (int q = st + l; q < cnt; q += 64) t += s_prod[q];")
+    w("for (int q = st + l; q < qhi; q += 64) t += s_prod[q];")
     w("t = tg_segsum<64>(t);")
     w("double tot = t;")
     w.open("if (tg_mp_commit(tg_part, e, ef, el, t, &tot) && l == 0 && rb < row_end)")
@@ -1414,9 +1598,9 @@ __device__ tg_i64 tg_st_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 
     w("#pragma unroll 1")
     w.open("for (int i = slot; i < nb; i += %d)" % SLOTS)
     w("const tg_i64 rs = s_ptr[i], re = s_ptr[i + 1];")
-    w("const int st = (int)((rs > p0 ? rs : p0) - p0), en = (int)(re - p0);")
+    w("const int st = (int)((rs > p0 ? rs : p0) - pa), en = (int)(re - pa);")
     w("const bool mine = !(b0 + i == ra && ra_cut);  // a cut ra was committed above")
-    w("const bool own = mine && en - st <= 64;")
+    w("const bool own = mine && en - st <= 64 && en <= qhi;  // staged whole")
     w("double acc = 0.0;")
     w.open("if (own)")
     w("#pragma unroll 4")
@@ -1435,10 +1619,11 @@ __device__ tg_i64 tg_st_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 
     w.open("for (int k = wv; k < nl; k += %d)" % WAVES)
     w("const int i = s_long[k];")
     w("const tg_i64 rs = s_ptr[i], re = s_ptr[i + 1];")
-    w("const int st = (int)((rs > p0 ? rs : p0) - p0), en = (int)(re - p0);")
+    w("const int st = (int)((rs > p0 ? rs : p0) - pa), en = (int)(re - pa);")
     w("double acc = 0.0;")
     w("#pragma unroll 4")
-    w("for (int q = st + l; q < en; q += 64) acc += s_prod[q];")
+    w("for (int q = st + l; q < (en < qhi ? en : qhi); q += 64) acc += s_prod[q];")
+    tail("ps > rs ? ps : rs", "re", "acc")
     w("acc = tg_segsum<64>(acc);")
     w.open("if (l == 0 && b0 + i < row_end)")
     store("acc", "b0 + i")
@@ -1450,8 +1635,9 @@ __device__ tg_i64 tg_st_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 
     w("// 4. row rb, when it begins in this range and reaches past the scratch's last range:")
     w("// summed whole by the whole workgroup with its own loads, the waves' sums added in")
     w("// wave order (the condition is the same for every wave)")
-    w.open("if (rb < n_rows && rb_s < p1 && rb_s / %d == e && (rb_e - 1) / %d >= %d)"
-           % (CH, CH, MERGE_CAP))
+    w.open("if (rb < n_rows && rb_s < p1 && (rb_s - pal) / %d == e && "
+           "((rb_e - 1 - pal) / %d < NL - 1 ? (rb_e - 1 - pal) / %d : NL - 1) >= %d)"
+           % (CH, CH, CH, MERGE_CAP))
     w("double t = 0.0;")
     w("#pragma unroll 4")
     w.open("for (tg_i64 pq = rb_s + (tg_i64)threadIdx.x; pq < rb_e; pq += %d)" % B)
@@ -1519,11 +1705,13 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     col = plan.col_idx.name
     gathered = _gather_operand(plan)
 
-    def step(q: str, lo: str, hi: str, acc: str) -> None:
-        """Load U consecutive nonzeros at q (masked to [lo, hi)), gather, FMA."""
+    def step(q: str, lo: str, hi: str, acc: str, glo: str = "glo", ghi: str = "ghi") -> None:
+        """Load U consecutive nonzeros at q (masked to [lo, hi)), gather, FMA.
+        Loads touch only positions in [glo, ghi) (the tile's nonzeros, or the
+        row's where no tile is staged), which hold [lo, hi)."""
         w("tg_i64 ci[%d]; double cv[%d];" % (U, U))
         if U % 2 == 0:
-            w.open("if (pair_ok && %s + %d <= nnz)" % (q, U))
+            w.open("if (pair_ok && %s >= %s && %s + %d <= %s)" % (q, glo, q, U, ghi))
             for u in range(0, U, 2):
                 w("{ const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + %s + %d));"
                   " ci[%d] = a.x; ci[%d] = a.y; }" % (q, u, u, u + 1))
@@ -1534,10 +1722,10 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         else:
             w.open("")
         for u in range(U):
-            w("ci[%d] = %s + %d < nnz ? __builtin_nontemporal_load(indices + %s + %d) : 0;"
-              % (u, q, u, q, u))
-            w("cv[%d] = %s + %d < nnz ? __builtin_nontemporal_load(data + %s + %d) : 0.0;"
-              % (u, q, u, q, u))
+            w("ci[%d] = ((%s + %d >= %s) & (%s + %d < %s)) ? "
+              "__builtin_nontemporal_load(indices + %s + %d) : 0;" % (u, q, u, glo, q, u, ghi, q, u))
+            w("cv[%d] = ((%s + %d >= %s) & (%s + %d < %s)) ? "
+              "__builtin_nontemporal_load(data + %s + %d) : 0.0;" % (u, q, u, glo, q, u, ghi, q, u))
         w.close()
         w("double xv[%d]; bool ok[%d];" % (U, U))
         w("// positions outside the row gather element 0 (every gather of the step is issued")
@@ -1600,7 +1788,7 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
             w("__shared__ int s_nmed;")
         w("__shared__ double s_red[%d];" % WAVES)
         if merge:
-            _merge_window(w, TR, WAVES)
+            _merge_window(w, TR, WAVES, plan)
             w.open("for (tg_i64 row0 = r0; row0 < r_own; row0 += %d)" % TR)
             w("const tg_i64 row_end = row0 + %d < r_own ? row0 + %d : r_own;" % (TR, TR))
         w("if (threadIdx.x == 0) { s_nlong = 0;%s }" % (" s_nmed = 0;" if wave_tier else ""))
@@ -1608,7 +1796,20 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("const tg_i64 r = row0 + t;")
         w("s_ptr[t] = indptr[r < row_end ? r : row_end];")
         w.close()
+        if hybrid:
+            w("// indptr[0] and indptr[M] with the row pointers: which long rows have ranges")
+            w("__shared__ tg_i64 s_lim[2];")
+            w("if (threadIdx.x == %d) s_lim[0] = indptr[0];" % (B - 1))
+            w("if (threadIdx.x == %d) s_lim[1] = indptr[%s];" % (B - 2 if B > 64 else B - 1,
+                                                                plan.row_extent))
         w("__syncthreads();")
+        w("// this tile's nonzeros: its loads touch no position outside them")
+        w("const tg_i64 glo = tg_uniform(s_ptr[0]), ghi = tg_uniform(s_ptr[%d]);" % TR)
+        if hybrid:
+            w("const tg_i64 pbase = tg_uniform(s_lim[0]), pend = tg_uniform(s_lim[1]);")
+            w("const tg_i64 pal = pbase & ~(tg_i64)1;")
+            w("const tg_i64 NR = pend > pbase ? (pend - pal + %d) / %d : 0;" % (CH - 1, CH))
+            w("const tg_i64 NL = NR < GL ? NR : GL;  // the ranges that exist")
         if wave_tier:
             w("// rows and nonzeros of this tile (s_ptr[%d] is clamped to the last row)" % TR)
             w("const tg_i64 t_rows = row_end - row0 < %d ? row_end - row0 : %d;" % (TR, TR))
@@ -1632,7 +1833,8 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     if coop:
         skip = ""
         if hybrid:
-            w("const bool lw = re[r] - rs[r] > %d;  // summed by the long-row workgroups" % LH)
+            w("// summed by the long-row workgroups, when its first range exists")
+            w("const bool lw = re[r] - rs[r] > %d && (rs[r] - pal) / %d < NL;" % (LH, CH))
             skip = "lw || "
         if wave_tier:
             w("const tg_i64 len = re[r] - rs[r];")
@@ -1666,7 +1868,7 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("(void)row;")
         w("const tg_i64 q = (rs[r] & ~(tg_i64)%d) + (tg_i64)lane * %d;" % (ALIGN - 1, U))
         w.open("if (q < re[r] && rs[r] < re[r])")
-        step("q", "rs[r]", "re[r]", "acc[r]")
+        step("q", "rs[r]", "re[r]", "acc[r]", *(() if low.tiled else ("rs[r]", "re[r]")))
         w.close()
         w.close()
     else:
@@ -1680,7 +1882,7 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("for (int u = 0; u < %d; ++u) { fci[r][u] = 0; fcv[r][u] = 0.0; }" % U)
         w.open("if (q < re[r] && rs[r] < re[r])")
         if U % 2 == 0:
-            w.open("if (pair_ok && q + %d <= nnz)" % U)
+            w.open("if (pair_ok && q >= glo && q + %d <= ghi)" % U)
             for u in range(0, U, 2):
                 w("{ const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + q + %d));"
                   " fci[r][%d] = a.x; fci[r][%d] = a.y; }" % (u, u, u + 1))
@@ -1691,12 +1893,14 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         else:
             w.open("")
         for u in range(U):
-            w("fci[r][%d] = q + %d < nnz ? __builtin_nontemporal_load(indices + q + %d) : 0;" % (u, u, u))
-            w("fcv[r][%d] = q + %d < nnz ? __builtin_nontemporal_load(data + q + %d) : 0.0;" % (u, u, u))
+            w("fci[r][%d] = ((q + %d >= glo) & (q + %d < ghi)) ? "
+              "__builtin_nontemporal_load(indices + q + %d) : 0;" % (u, u, u, u))
+            w("fcv[r][%d] = ((q + %d >= glo) & (q + %d < ghi)) ? "
+              "__builtin_nontemporal_load(data + q + %d) : 0.0;" % (u, u, u, u))
         w.close()
         w.close()
         w.close()
-        w.open("if (nnz > 0)")
+        w.open("if (ghi > glo)")
         w("double fxv[%d][%d]; bool fok[%d][%d];" % (R, U, R, U))
         w("#pragma unroll")
         w.open("for (int r = 0; r < %d; ++r)" % R)
@@ -1730,7 +1934,7 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w("#pragma unroll 1")
     w.open("for (tg_i64 q = (rs[r] & ~(tg_i64)%d) + (tg_i64)lane * %d + %d; q < re[r]; q += %d)"
            % (ALIGN - 1, U, STEP, STEP))
-    step("q", "rs[r]", "re[r]", "acc[r]")
+    step("q", "rs[r]", "re[r]", "acc[r]", *(() if low.tiled else ("rs[r]", "re[r]")))
     w.close()
     w.close()
     w("#pragma unroll")
@@ -1809,13 +2013,14 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w("if (!(k == 0 ? pc_in : pc_out)) continue;")
     w("const tg_i64 row = k == 0 ? r0 - 1 : r1 - 1;")
     w("const tg_i64 pb = k == 0 ? s_win[2] : s_win[4], pe = k == 0 ? s_win[3] : s_win[5];")
-    w("const tg_i64 c0 = k == 0 && t0 - row > pb ? t0 - row : pb;")
-    w("const tg_i64 c1 = t1 - row < pe ? t1 - row : pe;")
+    w("// item t of the row is its position t - row + pbase")
+    w("const tg_i64 c0 = k == 0 && t0 - row + pbase > pb ? t0 - row + pbase : pb;")
+    w("const tg_i64 c1 = t1 - row + pbase < pe ? t1 - row + pbase : pe;")
     w("double cacc = 0.0;")
     w("#pragma unroll 1")
     w.open("for (tg_i64 q = (c0 & ~(tg_i64)%d) + (tg_i64)threadIdx.x * %d; q < c1; q += %d)"
            % (ALIGN - 1, U, B * U))
-    step("q", "c0", "c1", "cacc")
+    step("q", "c0", "c1", "cacc", "pb", "pe")
     w.close()
     w("cacc = tg_segsum<64>(cacc);")
     w("if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = cacc;")
@@ -1824,7 +2029,8 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w("double t = 0.0;")
     w("#pragma unroll")
     w("for (int v = 0; v < %d; ++v) t += s_red[v];" % WAVES)
-    w("const tg_i64 wf = (row + pb) / D, wl = (row + pe - 1) / D;  // its first/last window")
+    w("const tg_i64 wf = (row + pb - pbase) / D, wl = (row + pe - 1 - pbase) / D;  "
+      "// its first/last window")
     w("double tot;")
     w.open("if (tg_mp_commit(tg_part, wdx, wf, wl, t, &tot) && threadIdx.x == 0)")
     env = _Env({row: "row"}, acc="tot")
@@ -2375,9 +2581,10 @@ def _check_hip_dtype(config: Config) -> None:
 
 def _grid_text(geo: LaunchGeometry) -> str:
     if geo.stream:
-        return "ceil(nnz / %d) (1 without nonzeros; 0 without rows)" % geo.nnz_chunk
+        return "floor(nnz / %d) + 1 (0 without rows)" % geo.nnz_chunk
     return "ceil(%s / %d)%s" % (geo.rows_symbol, geo.rows_per_block,
-                                " + ceil(nnz / %d)" % geo.nnz_chunk if geo.nnz_chunk else "")
+                                " + floor(nnz / %d) + 1" % geo.nnz_chunk if geo.nnz_chunk
+                                else "")
 
 
 def emit_hip(kernel: Kernel, config: Config, scratch_arg: bool = False) -> str:
@@ -2399,7 +2606,7 @@ def emit_hip(kernel: Kernel, config: Config, scratch_arg: bool = False) -> str:
     _sig, args, _info = abi_of(kernel)
     geo = launch_geometry(plan, low)
     extra = ["target      : %s (wave%d)" % (HIP_ARCH, WAVE),
-             "launch      : grid = %s, block = %d, lds = %d B"
+             "launch      : grid = %s, block = %d, static lds = %d B, dynamic lds = 0"
              % (_grid_text(geo), geo.block, geo.lds_bytes)]
     return "\n".join([_header(kernel, config, "hip", low, extra), _HIP_PRELUDE.strip(), "",
                       _hip_kernel_text(kernel, config, plan, low, args, geo, scratch_arg), ""])
@@ -2439,7 +2646,7 @@ def emit_hip_host(kernel: Kernel, config: Config) -> str:
     nnz = "nnz" if "nnz" in dims else "0"
     params = ", ".join("%s %s" % a for a in args)
     text = """/* TileGen HIP launcher for %(sym)s -- generated, DO NOT EDIT.
- * schedule %(sched)s; grid = %(grid_text)s, block = %(block)d, lds = %(lds)d B */
+ * schedule %(sched)s; grid = %(grid_text)s, block = %(block)d, static lds = %(lds)d B */
 #include <stdint.h>
 #include <string.h>
 #include "tgrt.h"
@@ -2466,7 +2673,9 @@ int tgv_geometry(int64_t M, int64_t N, int64_t K, int64_t nnz,
   const int64_t rows = %(rows_expr)s;
   *grid = %(grid_expr)s;%(extra)s
   *block = %(block)d;
-  *lds = %(lds)d;
+  /* dynamic LDS: none, the kernel declares its %(lds)d bytes of LDS statically (a
+     launch that passed them again would reserve them twice per workgroup) */
+  *lds = 0;
   return 0;
 }
 
@@ -2496,8 +2705,8 @@ int tgv_launch_async(void* stream, %(params)s) {
         "pack": "\n".join(pack), "nargs": len(args), "names": ", ".join(names),
         "sig": sig, "M": "M" if "M" in dims else "0", "N": ndim, "K": kdim, "nnz": nnz,
         "grid_text": _grid_text(geo),
-        "grid_expr": ("rows > 0 ? (nnz > 0 ? (nnz + %d - 1) / %d : 1) : 0"
-                      % (geo.nnz_chunk, geo.nnz_chunk) if geo.stream else
+        "grid_expr": ("rows > 0 ? (nnz > 0 ? nnz : 0) / %d + 1 : 0"
+                      % geo.nnz_chunk if geo.stream else
                       "rows > 0 ? (rows + %d - 1) / %d : 0" % (geo.rows_per_block,
                                                              geo.rows_per_block)),
         "launch": ("\n  /* row pieces are combined through this module's scratch, which one launch"
@@ -2505,9 +2714,10 @@ int tgv_launch_async(void* stream, %(params)s) {
                    "\n  return tg_launch_ordered(tg_code, fn, grid, block, lds, a, n, stream, 0);"
                    if uses_scratch else
                    "\n  return tg_launch(fn, grid, block, lds, a, n, stream, 0);"),
-        "extra": ("\n  /* long-row workgroups of hybrid tiles, ahead of the row tiles */"
-                  "\n  if (*grid > 0 && nnz > 0) *grid += (nnz + %d - 1) / %d;"
-                  % (geo.nnz_chunk, geo.nnz_chunk)) if geo.nnz_chunk and not geo.stream else "",
+        "extra": ("\n  /* long-row workgroups of hybrid tiles, ahead of the row tiles: one per"
+                  "\n     range that nnz nonzeros can meet (ranges start at an even position) */"
+                  "\n  if (*grid > 0) *grid += (nnz > 0 ? nnz : 0) / %d + 1;"
+                  % geo.nnz_chunk) if geo.nnz_chunk and not geo.stream else "",
     }
     return text
 
