@@ -70,6 +70,9 @@ def _parse_config(text: str):
         if part in ("nnz", "rows", "hybrid", "stream"):  # what a tile holds (Config.balance)
             vals["balance"] = part
             continue
+        if part in ("sorted", "direct"):  # the order of a tile's gathers (Config.gather)
+            vals["gather"] = part
+            continue
         for key, name in (("TPR", "threads_per_row"), ("T", "tile_size"), ("U", "unroll"),
                           ("V", "vector_width"), ("B", "block_size")):
             if part.startswith(key) and part[len(key):].isdigit():
@@ -368,7 +371,8 @@ def main(argv=None) -> int:
     ap.add_argument("--config", default=None,
                     help="schedule override for the headline case, e.g. T128/TPR8/U2/V1/B256 "
                          "(append /nnz for merge-path windows, /hybrid for long-row "
-                         "workgroups, /stream for equal nonzero ranges)")
+                         "workgroups, /stream for equal nonzero ranges, /sorted for row "
+                         "tiles whose gathers are sorted in LDS)")
     ap.add_argument("--case-iters", type=int, default=200,
                     help="event-timed launches per config under 'cases'")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,

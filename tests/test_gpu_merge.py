@@ -30,7 +30,7 @@ from tilegen_amd import codegen as cg
 from tilegen_amd.codegen import Config
 from tilegen_amd.matrices import make_baseline
 from tilegen_amd.schedules import (HYBRID_TEST_SCHEDULES, MERGE_TEST_SCHEDULES,
-                                   STREAM_TEST_SCHEDULES, schedule_id)
+                                   SORTED_TEST_SCHEDULES, STREAM_TEST_SCHEDULES, schedule_id)
 from tilegen_amd.variant import Variant
 
 pytestmark = pytest.mark.gpu
@@ -60,7 +60,8 @@ def _again_onto_nan(kernel, cfg, A, first):
     assert np.array_equal(out, first)
 
 
-_BALANCED = MERGE_TEST_SCHEDULES + HYBRID_TEST_SCHEDULES + STREAM_TEST_SCHEDULES
+_BALANCED = (MERGE_TEST_SCHEDULES + HYBRID_TEST_SCHEDULES + STREAM_TEST_SCHEDULES
+             + SORTED_TEST_SCHEDULES)
 
 
 @pytest.mark.parametrize("cfg", _BALANCED, ids=[schedule_id(c) for c in _BALANCED])

@@ -33,7 +33,8 @@ import oracle
 from tests.util import ragged, rel_2, rel_inf
 from tilegen_amd import runtime as rt
 from tilegen_amd.schedules import (HYBRID_TEST_SCHEDULES, MERGE_TEST_SCHEDULES, NOALLOC_SCHEDULE,
-                                   STREAM_TEST_SCHEDULES, TEST_SCHEDULES, TUNED, schedule_id)
+                                   SORTED_TEST_SCHEDULES, STREAM_TEST_SCHEDULES, TEST_SCHEDULES,
+                                   TUNED, schedule_id)
 from tilegen_amd.variant import Variant
 
 pytestmark = pytest.mark.gpu
@@ -42,7 +43,8 @@ TOL = 1e-10
 
 SPMV_FORMS = [TUNED["c1"], TUNED["c2"], TEST_SCHEDULES[0], TEST_SCHEDULES[4],
               MERGE_TEST_SCHEDULES[1], MERGE_TEST_SCHEDULES[6], NOALLOC_SCHEDULE,
-              HYBRID_TEST_SCHEDULES[6], TUNED["c3a"], TUNED["c3b"], STREAM_TEST_SCHEDULES[2]]
+              HYBRID_TEST_SCHEDULES[6], TUNED["c3a"], TUNED["c3b"], STREAM_TEST_SCHEDULES[2],
+              SORTED_TEST_SCHEDULES[0], SORTED_TEST_SCHEDULES[3]]
 SCRATCH_FORMS = [TUNED["c3a"], TUNED["c3b"], STREAM_TEST_SCHEDULES[0], NOALLOC_SCHEDULE,
                  HYBRID_TEST_SCHEDULES[1], MERGE_TEST_SCHEDULES[1]]
 

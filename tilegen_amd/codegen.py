@@ -101,9 +101,13 @@ class Config:
     workgroups that each take an equal range of nonzeros) or ``"stream"`` (an
     equal range of B*U nonzeros and the rows that end in it; T is not used);
     the last three are for SpMV-shaped kernels (see ``_hip_scalar_reduce`` and
-    ``_hip_stream_reduce``).  It has no counterpart in
-    the reference and is left out of ``to_dict``/``hash`` at its default, so
-    every reference schedule keeps its name.
+    ``_hip_stream_reduce``).  ``gather`` is the order of a row tile's
+    first-step gathers: ``"direct"`` or ``"sorted"`` (made in the order of the
+    gathered operand, sorted in LDS, so that the lanes of one gather
+    instruction share cache lines; SpMV-shaped row tiles, see
+    ``_sorted_first_step``).  Neither has a counterpart in the reference; both
+    are left out of ``to_dict``/``hash`` at their defaults, so every reference
+    schedule keeps its name.
     """
 
     tile_size: int = 32
@@ -114,6 +118,7 @@ class Config:
     dtype: str = "f64"
     inject_bug: bool = False
     balance: str = "rows"
+    gather: str = "direct"
 
     def to_dict(self) -> Dict[str, Any]:
         d = {"tile_size": self.tile_size, "threads_per_row": self.threads_per_row,
@@ -122,23 +127,29 @@ class Config:
              "inject_bug": self.inject_bug}
         if self.balance != "rows":
             d["balance"] = self.balance
+        if self.gather != "direct":
+            d["gather"] = self.gather
         return d
 
     def hash(self) -> str:
         """sha1 of ``T|TPR|U|V|B|dtype|bug``, 10 hex digits (the reference's
         closed form, ``codegen.py:82-87``, so cache names line up); a
-        non-default ``balance`` is appended as ``|<balance>``."""
+        non-default ``balance`` is appended as ``|<balance>``, a non-default
+        ``gather`` as ``|gather=<gather>``."""
         key = "%d|%d|%d|%d|%d|%s|%d" % (self.tile_size, self.threads_per_row, self.unroll,
                                         self.vector_width, self.block_size, self.dtype,
                                         int(self.inject_bug))
         if self.balance != "rows":
             key += "|" + self.balance
+        if self.gather != "direct":
+            key += "|gather=" + self.gather
         return hashlib.sha1(key.encode()).hexdigest()[:10]
 
     def short(self) -> str:
-        return "T%d/TPR%d/U%d/V%d/B%d%s" % (self.tile_size, self.threads_per_row,
-                                            self.unroll, self.vector_width, self.block_size,
-                                            {"rows": ""}.get(self.balance, "/" + self.balance))
+        return "T%d/TPR%d/U%d/V%d/B%d%s%s" % (self.tile_size, self.threads_per_row,
+                                              self.unroll, self.vector_width, self.block_size,
+                                              {"rows": ""}.get(self.balance, "/" + self.balance),
+                                              "" if self.gather == "direct" else "/" + self.gather)
 
 
 @dataclass
@@ -157,6 +168,7 @@ class Lowering:
     parallel: bool = False
     tiled: bool = False
     balance: str = "rows"
+    gather: str = "direct"
 
     def to_dict(self) -> Dict[str, Any]:
         d = {"tile": self.tile, "threads_per_row": self.threads_per_row,
@@ -164,6 +176,8 @@ class Lowering:
              "block_size": self.block_size, "parallel": self.parallel}
         if self.balance != "rows":
             d["balance"] = self.balance
+        if self.gather != "direct":
+            d["gather"] = self.gather
         return d
 
 
@@ -171,7 +185,7 @@ def _lowering(kernel: Kernel) -> Lowering:
     low = Lowering()
     for t in kernel.schedule:
         if isinstance(t, Tile):
-            low.tile, low.tiled, low.balance = t.size, True, t.by
+            low.tile, low.tiled, low.balance, low.gather = t.size, True, t.by, t.gather
         elif isinstance(t, ThreadsPerRow):
             low.threads_per_row = t.k
         elif isinstance(t, Unroll):
@@ -606,9 +620,9 @@ def _cpu_body(kernel: Kernel, config: Config, plan: Plan, low: Lowering) -> str:
 # --------------------------------------------------------------------------- #
 def _transform_text(t) -> str:
     if isinstance(t, Tile):
-        if t.by != "rows":
-            return "Tile(%s,%d,%s)" % (t.index.name, t.size, t.by)
-        return "Tile(%s,%d)" % (t.index.name, t.size)
+        extra = ("," + t.by if t.by != "rows" else "") + \
+            (",gather=" + t.gather if t.gather != "direct" else "")
+        return "Tile(%s,%d%s)" % (t.index.name, t.size, extra)
     if isinstance(t, Split):
         return "Split(%s,%d)" % (t.index.name, t.factor)
     if isinstance(t, Parallelize):
@@ -727,6 +741,11 @@ def launch_geometry(plan: Plan, low: Lowering) -> LaunchGeometry:
         lds = 8 * CH + 8 * (RB + 1) + 4 * RB + 8 * 6 + 4 + 8 * max(1, B // WAVE)
         return LaunchGeometry(1, B, lds, plan.row_extent, CH, stream=True)
     lds = 8 * (rows + 1) if (plan.kind == "scalar_reduce" and low.tiled) else 0
+    if plan.kind == "scalar_reduce" and low.tiled and low.gather == "sorted":
+        # the sort's bucket counts, sorted entries and operands (sort_buckets)
+        items = ((rows + slots - 1) // slots) * max(1, low.unroll) * B
+        nb = sort_buckets(B)
+        lds += 4 * nb + 16 * items + 4 * (nb // 64)
     chunk = hybrid_chunk(low) if (plan.kind == "scalar_reduce" and low.tiled
                                   and low.balance == "hybrid") else 0
     return LaunchGeometry(rows, B, lds, plan.row_extent, chunk)
@@ -787,6 +806,9 @@ def _check_hip_schedule(plan: Plan, low: Lowering) -> None:
         raise ValueError("balance '%s' needs a tiled kernel that reduces over each row "
                          "(SpMV-shaped); %s %s" % (low.balance, plan.kind,
                                                    "untiled" if not low.tiled else ""))
+    if low.gather != "direct" and not (plan.kind == "scalar_reduce" and low.tiled
+                                       and low.balance == "rows"):
+        raise ValueError("gather '%s' needs an SpMV-shaped kernel with row tiles" % low.gather)
     if low.balance == "stream" and stream_chunk(low) > STREAM_MAX_CHUNK:
         raise ValueError("stream ranges hold at most %d nonzeros (block_size x unroll), got %d"
                          % (STREAM_MAX_CHUNK, stream_chunk(low)))
@@ -1656,6 +1678,106 @@ __device__ tg_i64 tg_st_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 
     w.close()
 
 
+SORT_MAX_ITEMS = 8192   # slots of a sorted tile's first step (13 bits in an LDS entry)
+
+
+def sort_buckets(block: int) -> int:
+    """Buckets of a sorted tile: the largest power of two <= the workgroup
+    (at least one wave)."""
+    nb = 64
+    while nb * 2 <= block:
+        nb *= 2
+    return nb
+
+
+def _sorted_first_step(w: _W, plan: Plan, R: int, U: int, B: int, SLOTS: int,
+                       fpos: Callable[[str, int], str], row: str) -> None:
+    """The tile's first-step gathers in operand order (``gather == "sorted"``).
+
+    Every lane holds R x U first-step nonzeros (fci/fcv), slot
+    (r U + u) B + threadIdx.x of the tile.  Their columns are counting-sorted
+    in LDS by bucket col >> sshift (NB buckets): an atomic add per item gives
+    its rank in its bucket, an exclusive scan gives the buckets' offsets, and
+    each item writes (col << 13 | slot) to its sorted place.  Lane t then takes
+    the sorted items k B + t, so the 64 lanes of a gather instruction take 64
+    consecutive sorted items and share lines of the operand, and stores each
+    operand in s_x at the item's slot.  Each lane reads its own items' operands
+    back and sums them in the order of the direct gathers, so the result bits
+    are the same.  Positions outside their row take part in nothing."""
+    gathered = _gather_operand(plan)
+    NB = sort_buckets(B)
+    w("// this tile's first-step nonzeros, sorted by operand bucket (col >> sshift)")
+    w("bool fok[%d][%d]; int fky[%d][%d]; unsigned frk[%d][%d];" % (R, U, R, U, R, U))
+    w("#pragma unroll")
+    w.open("for (int r = 0; r < %d; ++r)" % R)
+    for u in range(U):
+        w.open("")
+        w("const tg_i64 pu = %s;" % fpos("rs[r]", u))
+        w("fok[r][%d] = (pu >= rs[r]) & (pu < re[r]);" % u)
+        w.close()
+    w("#pragma unroll")
+    w.open("for (int u = 0; u < %d; ++u)" % U)
+    w("fky[r][u] = fok[r][u] ? (int)(fci[r][u] >> sshift) : 0;")
+    w("frk[r][u] = fok[r][u] ? atomicAdd(&s_hist[fky[r][u]], 1u) : 0u;  // rank in its bucket")
+    w.close()
+    w.close()
+    w("__syncthreads();")
+    w("// exclusive scan of the %d buckets: each wave's, then the waves' totals" % NB)
+    w("unsigned sh_ = 0u, sv_ = 0u;")
+    w.open("if (threadIdx.x < %d)" % NB)
+    w("sh_ = s_hist[threadIdx.x];")
+    w("sv_ = sh_;")
+    w("#pragma unroll")
+    w.open("for (int d = 1; d < 64; d <<= 1)")
+    w("const unsigned o = __shfl_up(sv_, d);")
+    w("if ((threadIdx.x & 63) >= d) sv_ += o;")
+    w.close()
+    w("if ((threadIdx.x & 63) == 63) s_swsum[threadIdx.x >> 6] = sv_;")
+    w.close()
+    w("__syncthreads();")
+    w("unsigned nsort = 0u, sbase = 0u;")
+    w("#pragma unroll")
+    w.open("for (int v = 0; v < %d; ++v)" % (NB // 64))
+    w("if (v < (int)(threadIdx.x >> 6)) sbase += s_swsum[v];")
+    w("nsort += s_swsum[v];")
+    w.close()
+    w("if (threadIdx.x < %d) s_hist[threadIdx.x] = sbase + sv_ - sh_;" % NB)
+    w("__syncthreads();")
+    w("#pragma unroll")
+    w.open("for (int r = 0; r < %d; ++r)" % R)
+    w("#pragma unroll")
+    w.open("for (int u = 0; u < %d; ++u)" % U)
+    w("if (fok[r][u]) s_ent[s_hist[fky[r][u]] + frk[r][u]] = "
+      "((unsigned long long)fci[r][u] << 13) | (unsigned)((r * %d + u) * %d + threadIdx.x);"
+      % (U, B))
+    w.close()
+    w.close()
+    w("__syncthreads();")
+    w("// the gathers, 64 consecutive sorted items per instruction")
+    w("#pragma unroll")
+    w.open("for (int k = 0; k < %d; ++k)" % (R * U))
+    w("const unsigned sk = (unsigned)(k * %d) + threadIdx.x;" % B)
+    w.open("if (sk < nsort)")
+    w("const unsigned long long e = s_ent[sk];")
+    w("const tg_i64 cu = (tg_i64)(e >> 13);")
+    w("s_x[e & 8191u] = %s;" % _cexpr(gathered, _Env({row: "0", plan.col_idx.name: "cu"},
+                                                         p="0")))
+    w.close()
+    w.close()
+    w("__syncthreads();")
+    w("#pragma unroll")
+    w.open("for (int r = 0; r < %d; ++r)" % R)
+    w("const tg_i64 row = row0 + slot + r * %d;" % SLOTS)
+    w("(void)row;")
+    w("#pragma unroll")
+    w.open("for (int u = 0; u < %d; ++u)" % U)
+    w("const double xs_ = fok[r][u] ? s_x[(r * %d + u) * %d + threadIdx.x] : 0.0;" % (U, B))
+    w("acc[r] = fok[r][u] ? acc[r] + %s : acc[r];"
+      % _value_with(plan, "fcv[r][u]", "xs_", row, "fci[r][u]"))
+    w.close()
+    w.close()
+
+
 def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: LaunchGeometry,
                        out_name: str, pre: Optional[_W] = None,
                        scratch_arg: bool = False) -> None:
@@ -1744,8 +1866,81 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
                                                                    "ci[u]"), acc))
         w.close()
 
+    # positions of a lane's first-step nonzeros: U consecutive ones, or, where a lane
+    # group holds several rows' first steps at once (R > 1, U >= 4 even), its U / 2
+    # pairs interleaved with the other lanes of its group (pair k at 2 lane + 2 TPR k),
+    # so that a pair-load instruction covers whole lines
+    IL = U % 2 == 0 and U >= 4 and R > 1
+
+    def fpos(base: str, u: int) -> str:
+        if IL:
+            return "((%s) & ~(tg_i64)1) + 2 * (tg_i64)lane + %d" % (base, (u // 2) * 2 * TPR
+                                                                     + u % 2)
+        return "((%s) & ~(tg_i64)%d) + (tg_i64)lane * %d + %d" % (base, ALIGN - 1, U, u)
+
+    def first_loads(rs_: str, re_: str, lo: str, hi: str) -> None:
+        """Row r's first-step nonzeros into fci[r]/fcv[r] (zero outside the row),
+        loading no position outside [lo, hi)."""
+        if IL:
+            for k in range(U // 2):
+                w.open("")
+                w("const tg_i64 q = %s;" % fpos(rs_, 2 * k))
+                w("fci[r][%d] = 0; fcv[r][%d] = 0.0; fci[r][%d] = 0; fcv[r][%d] = 0.0;"
+                  % (2 * k, 2 * k, 2 * k + 1, 2 * k + 1))
+                w.open("if (q < %s && %s < %s)" % (re_, rs_, re_))
+                w.open("if (pair_ok && q >= %s && q + 2 <= %s)" % (lo, hi))
+                w("{ const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + q));"
+                  " fci[r][%d] = a.x; fci[r][%d] = a.y; }" % (2 * k, 2 * k + 1))
+                w("{ const tg_f64x2 b = __builtin_nontemporal_load((const tg_f64x2*)(data + q));"
+                  " fcv[r][%d] = b.x; fcv[r][%d] = b.y; }" % (2 * k, 2 * k + 1))
+                w.close()
+                w.open("else")
+                for d in (0, 1):
+                    w("fci[r][%d] = ((q + %d >= %s) & (q + %d < %s)) ? "
+                      "__builtin_nontemporal_load(indices + q + %d) : 0;"
+                      % (2 * k + d, d, lo, d, hi, d))
+                    w("fcv[r][%d] = ((q + %d >= %s) & (q + %d < %s)) ? "
+                      "__builtin_nontemporal_load(data + q + %d) : 0.0;"
+                      % (2 * k + d, d, lo, d, hi, d))
+                w.close()
+                w.close()
+                w.close()
+            return
+        w("const tg_i64 q = (%s & ~(tg_i64)%d) + (tg_i64)lane * %d;" % (rs_, ALIGN - 1, U))
+        w("#pragma unroll")
+        w("for (int u = 0; u < %d; ++u) { fci[r][u] = 0; fcv[r][u] = 0.0; }" % U)
+        w.open("if (q < %s && %s < %s)" % (re_, rs_, re_))
+        if U % 2 == 0:
+            w.open("if (pair_ok && q >= %s && q + %d <= %s)" % (lo, U, hi))
+            for u in range(0, U, 2):
+                w("{ const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + q + %d));"
+                  " fci[r][%d] = a.x; fci[r][%d] = a.y; }" % (u, u, u + 1))
+                w("{ const tg_f64x2 b = __builtin_nontemporal_load((const tg_f64x2*)(data + q + %d));"
+                  " fcv[r][%d] = b.x; fcv[r][%d] = b.y; }" % (u, u, u + 1))
+            w.close()
+            w.open("else")
+        else:
+            w.open("")
+        for u in range(U):
+            w("fci[r][%d] = ((q + %d >= %s) & (q + %d < %s)) ? "
+              "__builtin_nontemporal_load(indices + q + %d) : 0;" % (u, u, lo, u, hi, u))
+            w("fcv[r][%d] = ((q + %d >= %s) & (q + %d < %s)) ? "
+              "__builtin_nontemporal_load(data + q + %d) : 0.0;" % (u, u, lo, u, hi, u))
+        w.close()
+        w.close()
+
     merge = coop and low.balance == "nnz"
     hybrid = coop and low.balance == "hybrid"
+    sorted_ = low.gather == "sorted"
+    if sorted_:
+        if not (coop and low.balance == "rows"):
+            raise ValueError("gather 'sorted' needs row tiles (a tile and balance 'rows')")
+        if R * U > 8 or R * U * B > SORT_MAX_ITEMS:
+            raise ValueError("gather 'sorted' holds a tile's first step in registers: rows "
+                             "per lane group x unroll (%d x %d) must be <= 8" % (R, U))
+        if not _value_row_free(plan):
+            raise ValueError("gather 'sorted' needs a per-nonzero value that reads only the "
+                             "sparse value and the gathered operand")
     if merge or hybrid:
         if pre is None:
             raise ValueError("merge-path and hybrid tiles need file-scope declarations")
@@ -1791,6 +1986,50 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
             _merge_window(w, TR, WAVES, plan)
             w.open("for (tg_i64 row0 = r0; row0 < r_own; row0 += %d)" % TR)
             w("const tg_i64 row_end = row0 + %d < r_own ? row0 + %d : r_own;" % (TR, TR))
+        if sorted_:
+            NB = sort_buckets(B)
+            w("// the first step's gathers, sorted: bucket counts, sorted entries, operands")
+            w("__shared__ unsigned s_hist[%d];" % NB)
+            w("__shared__ unsigned long long s_ent[%d];" % (R * U * B))
+            w("__shared__ double s_x[%d];" % (R * U * B))
+            w("__shared__ unsigned s_swsum[%d];" % (NB // 64))
+            w("// buckets of 2^sshift columns of the operand: fewer than %d of them" % NB)
+            w("const tg_i64 ncol_ = %s;" % _extent_for(plan, plan.col_idx.name))
+            w("const int sshift = ncol_ > %d ? 64 - __clzll((unsigned long long)(ncol_ - 1)) - %d"
+              " : 0;" % (NB, NB.bit_length() - 1))
+            w("if (threadIdx.x < %d) s_hist[threadIdx.x] = 0u;" % NB)
+        if sorted_:
+            w("// Before the row pointers, each row's first step is loaded where rows of Ls =")
+            w("// nnz / M nonzeros each from position 0 would put it, when nnz is such a multiple")
+            w("// of M that every lane's 128-bit pairs lie inside its row (positions below nnz,")
+            w("// with no per-lane condition, so they issue back to back).  Rows whose bounds")
+            w("// turn out otherwise load again once the row pointers have arrived.")
+            w("tg_i64 Ls = nnz > 0 && %s > 0 && nnz %% %s == 0 ? nnz / %s : 0;"
+              % (plan.row_extent, plan.row_extent, plan.row_extent))
+            w("tg_i64 fci[%d][%d]; double fcv[%d][%d]; tg_i64 gs[%d];" % (R, U, R, U, R))
+            if U % 2 == 0:
+                w("if (!(pair_ok && Ls >= %d && (Ls & 1) == 0)) Ls = 0;" % (TPR * U))
+            else:
+                w("Ls = 0;  // odd unroll: no 128-bit pairs to guess with")
+            w("#pragma unroll")
+            w.open("for (int r = 0; r < %d; ++r)" % R)
+            w("const int lr = slot + r * %d;" % SLOTS)
+            w("const tg_i64 grow = row0 + lr;")
+            w("gs[r] = lr < %d && grow < row_end ? grow * Ls : -1;" % TR)
+            w.close()
+            if U % 2 == 0:
+                w.open("if (Ls > 0)")
+                w("#pragma unroll")
+                w.open("for (int r = 0; r < %d; ++r)" % R)
+                w("const tg_i64 gb = gs[r] >= 0 ? gs[r] : 0;")
+                for u in range(0, U, 2):
+                    w("{ const tg_i64 q = %s;" % fpos("gb", u))
+                    w("  const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + q));"
+                      " fci[r][%d] = a.x; fci[r][%d] = a.y;" % (u, u + 1))
+                    w("  const tg_f64x2 b = __builtin_nontemporal_load((const tg_f64x2*)(data + q));"
+                      " fcv[r][%d] = b.x; fcv[r][%d] = b.y; }" % (u, u + 1))
+                w.close()
+                w.close()
         w("if (threadIdx.x == 0) { s_nlong = 0;%s }" % (" s_nmed = 0;" if wave_tier else ""))
         w.open("for (int t = threadIdx.x; t <= %d; t += %d)" % (TR, B))
         w("const tg_i64 r = row0 + t;")
@@ -1860,7 +2099,7 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
 
     # every row's first step held at once costs about 6 R U registers per lane: past
     # R U = 8 that spills, so such schedules keep one guarded step per row
-    if R == 1 or R * U > 8:
+    if (R == 1 and not sorted_) or R * U > 8:
         w("// first step of every row in flight before any accumulation")
         w("#pragma unroll")
         w.open("for (int r = 0; r < %d; ++r)" % R)
@@ -1874,57 +2113,58 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     else:
         w("// first step of every row: every row's loads, then every row's gathers (none")
         w("// behind a per-lane condition, so they issue back to back), then the sums")
-        w("tg_i64 fci[%d][%d]; double fcv[%d][%d];" % (R, U, R, U))
-        w("#pragma unroll")
-        w.open("for (int r = 0; r < %d; ++r)" % R)
-        w("const tg_i64 q = (rs[r] & ~(tg_i64)%d) + (tg_i64)lane * %d;" % (ALIGN - 1, U))
-        w("#pragma unroll")
-        w("for (int u = 0; u < %d; ++u) { fci[r][u] = 0; fcv[r][u] = 0.0; }" % U)
-        w.open("if (q < re[r] && rs[r] < re[r])")
-        if U % 2 == 0:
-            w.open("if (pair_ok && q >= glo && q + %d <= ghi)" % U)
-            for u in range(0, U, 2):
-                w("{ const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + q + %d));"
-                  " fci[r][%d] = a.x; fci[r][%d] = a.y; }" % (u, u, u + 1))
-                w("{ const tg_f64x2 b = __builtin_nontemporal_load((const tg_f64x2*)(data + q + %d));"
-                  " fcv[r][%d] = b.x; fcv[r][%d] = b.y; }" % (u, u, u + 1))
+        if sorted_:
+            w("// rows whose bounds are not the guessed ones load their first step now")
+            w("#pragma unroll")
+            w.open("for (int r = 0; r < %d; ++r)" % R)
+            w.open("if (!(Ls > 0 && rs[r] == gs[r] && re[r] == gs[r] + Ls))")
+            first_loads("rs[r]", "re[r]", "glo", "ghi")
             w.close()
-            w.open("else")
+            w.close()
         else:
-            w.open("")
-        for u in range(U):
-            w("fci[r][%d] = ((q + %d >= glo) & (q + %d < ghi)) ? "
-              "__builtin_nontemporal_load(indices + q + %d) : 0;" % (u, u, u, u))
-            w("fcv[r][%d] = ((q + %d >= glo) & (q + %d < ghi)) ? "
-              "__builtin_nontemporal_load(data + q + %d) : 0.0;" % (u, u, u, u))
-        w.close()
-        w.close()
-        w.close()
+            w("tg_i64 fci[%d][%d]; double fcv[%d][%d];" % (R, U, R, U))
+            w("#pragma unroll")
+            w.open("for (int r = 0; r < %d; ++r)" % R)
+            first_loads("rs[r]", "re[r]", "glo", "ghi")
+            w.close()
         w.open("if (ghi > glo)")
-        w("double fxv[%d][%d]; bool fok[%d][%d];" % (R, U, R, U))
-        w("#pragma unroll")
-        w.open("for (int r = 0; r < %d; ++r)" % R)
-        w("const tg_i64 row = row0 + slot + r * %d;" % SLOTS)
-        w("(void)row;")
-        w("const tg_i64 q = (rs[r] & ~(tg_i64)%d) + (tg_i64)lane * %d;" % (ALIGN - 1, U))
-        w("#pragma unroll")
-        w.open("for (int u = 0; u < %d; ++u)" % U)
-        w("const tg_i64 pu = q + u;")
-        w("fok[r][u] = (pu >= rs[r]) & (pu < re[r]);")
-        w("const tg_i64 cu = fok[r][u] ? fci[r][u] : 0;")
-        w("fxv[r][u] = %s;" % _cexpr(gathered, _Env({row: "row", col: "cu"}, p="pu")))
-        w.close()
-        w.close()
-        w("#pragma unroll")
-        w.open("for (int r = 0; r < %d; ++r)" % R)
-        w("const tg_i64 row = row0 + slot + r * %d;" % SLOTS)
-        w("(void)row;")
-        w("#pragma unroll")
-        w.open("for (int u = 0; u < %d; ++u)" % U)
-        w("acc[r] = fok[r][u] ? acc[r] + %s : acc[r];"
-          % _value_with(plan, "fcv[r][u]", "fxv[r][u]", row, "fci[r][u]"))
-        w.close()
-        w.close()
+        if sorted_:
+            _sorted_first_step(w, plan, R, U, B, SLOTS, fpos, row)
+        else:
+            w("double fxv[%d][%d]; bool fok[%d][%d];" % (R, U, R, U))
+            w("#pragma unroll")
+            w.open("for (int r = 0; r < %d; ++r)" % R)
+            w("const tg_i64 row = row0 + slot + r * %d;" % SLOTS)
+            w("(void)row;")
+            if IL:
+                for u in range(U):
+                    w.open("")
+                    w("const tg_i64 pu = %s;" % fpos("rs[r]", u))
+                    w("fok[r][%d] = (pu >= rs[r]) & (pu < re[r]);" % u)
+                    w("const tg_i64 cu = fok[r][%d] ? fci[r][%d] : 0;" % (u, u))
+                    w("fxv[r][%d] = %s;" % (u, _cexpr(gathered, _Env({row: "row", col: "cu"},
+                                                                     p="pu"))))
+                    w.close()
+            else:
+                w("const tg_i64 q = (rs[r] & ~(tg_i64)%d) + (tg_i64)lane * %d;" % (ALIGN - 1, U))
+                w("#pragma unroll")
+                w.open("for (int u = 0; u < %d; ++u)" % U)
+                w("const tg_i64 pu = q + u;")
+                w("fok[r][u] = (pu >= rs[r]) & (pu < re[r]);")
+                w("const tg_i64 cu = fok[r][u] ? fci[r][u] : 0;")
+                w("fxv[r][u] = %s;" % _cexpr(gathered, _Env({row: "row", col: "cu"}, p="pu")))
+                w.close()
+            w.close()
+            w("#pragma unroll")
+            w.open("for (int r = 0; r < %d; ++r)" % R)
+            w("const tg_i64 row = row0 + slot + r * %d;" % SLOTS)
+            w("(void)row;")
+            w("#pragma unroll")
+            w.open("for (int u = 0; u < %d; ++u)" % U)
+            w("acc[r] = fok[r][u] ? acc[r] + %s : acc[r];"
+              % _value_with(plan, "fcv[r][u]", "fxv[r][u]", row, "fci[r][u]"))
+            w.close()
+            w.close()
         w.close()
     w("// remaining steps (rows longer than %d nonzeros)" % (STEP - ALIGN + 1))
     w("#pragma unroll")

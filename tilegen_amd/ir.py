@@ -220,6 +220,11 @@ class Tile(Transform):
     #: equal range of nonzeros per workgroup and the rows that end in it; ``size``
     #: is not used)
     by: str = "rows"
+    #: the order of a tile's gathers: ``direct`` (each lane gathers its own
+    #: nonzeros' operands) or ``sorted`` (the tile's first-step gathers are made in
+    #: operand order, sorted in LDS, so that one gather instruction's lanes share
+    #: cache lines)
+    gather: str = "direct"
     kind: ClassVar[str] = "tile"
 
 
@@ -465,6 +470,8 @@ def _check_transform(t: Transform, known: set) -> None:
         raise ValueError("transform %r factor/size must be > 0" % t.kind)
     if isinstance(t, Tile) and t.by not in ("rows", "nnz", "hybrid", "stream"):
         raise ValueError("tile 'by' must be 'rows', 'nnz', 'hybrid' or 'stream', got %r" % t.by)
+    if isinstance(t, Tile) and t.gather not in ("direct", "sorted"):
+        raise ValueError("tile 'gather' must be 'direct' or 'sorted', got %r" % t.gather)
     if isinstance(t, Split) and t.factor <= 0:
         raise ValueError("transform %r factor/size must be > 0" % t.kind)
     if isinstance(t, Unroll) and t.factor <= 0:
@@ -582,9 +589,9 @@ def _loop_nest_lines(kernel: Kernel) -> List[str]:
 
 def _transform_text(t: Transform) -> str:
     if isinstance(t, Tile):
-        if t.by != "rows":
-            return "Tile(%s, %d, by=%s)" % (t.index.name, t.size, t.by)
-        return "Tile(%s, %d)" % (t.index.name, t.size)
+        extra = (", by=%s" % t.by if t.by != "rows" else "") + \
+            (", gather=%s" % t.gather if t.gather != "direct" else "")
+        return "Tile(%s, %d%s)" % (t.index.name, t.size, extra)
     if isinstance(t, Split):
         return "Split(%s, %d)" % (t.index.name, t.factor)
     if isinstance(t, Parallelize):
@@ -659,6 +666,8 @@ def _transform_dump(t: Transform) -> Dict[str, Any]:
         out.update(index={"name": t.index.name}, size=t.size)
         if t.by != "rows":
             out.update(by=t.by)
+        if t.gather != "direct":
+            out.update(gather=t.gather)
     elif isinstance(t, (Split, Unroll)):
         out.update(index={"name": t.index.name}, factor=t.factor)
     elif isinstance(t, Parallelize):
@@ -676,7 +685,7 @@ def _transform_load(d: Dict[str, Any]) -> Transform:
     kind = d["kind"]
     ix = Index(d["index"]["name"]) if "index" in d else None
     if kind == "tile":
-        return Tile(ix, d["size"], d.get("by", "rows"))
+        return Tile(ix, d["size"], d.get("by", "rows"), d.get("gather", "direct"))
     if kind == "split":
         return Split(ix, d["factor"])
     if kind == "parallelize":

@@ -176,7 +176,8 @@ def tiling(kernel: Kernel) -> Kernel:
         _log(kernel, "tiling", "tile_size <= 1; no tiling applied")
         return kernel
     balance = getattr(getattr(kernel, "_config", None), "balance", "rows") or "rows"
-    _set_transform(kernel, Tile, same, Tile(outer, size, balance))
+    gather = getattr(getattr(kernel, "_config", None), "gather", "direct") or "direct"
+    _set_transform(kernel, Tile, same, Tile(outer, size, balance, gather))
     if balance == "hybrid":
         _log(kernel, "tiling",
              "strip-mined '%s' into tiles of %d rows; rows longer than a long-row "
@@ -201,6 +202,14 @@ def tiling(kernel: Kernel) -> Kernel:
              % (outer.name, size),
              "for %s in 0..extent" % outer.name,
              "for window w: for %s whose first nonzero is in w: ..." % outer.name)
+        return kernel
+    if gather == "sorted":
+        _log(kernel, "tiling",
+             "strip-mined '%s' into tiles of %d rows ('%s_o' over tiles, '%s_i' within); "
+             "each tile makes its first-step gathers in the order of the gathered operand, "
+             "sorted in LDS" % (outer.name, size, outer.name, outer.name),
+             "for %s in 0..extent" % outer.name,
+             "for %s_o step %d: sort gathers; for %s_i: ..." % (outer.name, size, outer.name))
         return kernel
     _log(kernel, "tiling",
          "strip-mined '%s' into tiles of %d rows ('%s_o' over tiles, '%s_i' within)"

@@ -23,7 +23,9 @@ Orders (how the host lays out each range of CH nonzeros before upload):
   64 consecutive items of the sorted range.  This is the order a kernel would
   reach by counting-sorting each range in LDS; the probe pays none of that
   sort, so it bounds what such a kernel could gain;
-* ``line``: the same with S = 4 (one 128-byte line of ``x`` per key).
+* ``line``: the same with S = 4 (one 128-byte line of ``x`` per key);
+* ``lsort``: the matrix order, sorted by the workgroup itself in LDS
+  (``lsort_source``): what the host-sorted orders bound, with the sort paid.
 
 Gather modes: ``x`` (``x[col]``), ``none`` (the index itself used as the
 operand, so the index loads stay live but nothing is gathered) and ``one``
@@ -93,6 +95,95 @@ def flat_source(name: str, blk: int, u: int, seg: int, gather: str) -> str:
               "  if (t %% %d == 0) out[((tg_i64)blockIdx.x * %d + t) / %d] = acc;" % (seg, blk, seg),
               "}"]
     return "\n".join(lines) + "\n"
+
+
+def lsort_source(name: str, blk: int, u: int, seg: int, nb: int) -> str:
+    """HIP source of the ``lsort`` probe: the flat probe's loads and sums, with
+    the gathers made in an order the workgroup sorts itself, in LDS.
+
+    Each of the BLK x U nonzeros of a range gets a slot s = u BLK + t.  Keys are
+    ``col >> shift`` (a kernel argument, so that NB buckets cover the columns):
+    an LDS histogram (atomic adds that return each item's rank in its bucket),
+    an exclusive scan over the NB buckets, then every item writes (col << 13 |
+    slot) to its sorted place.  Lane t then gathers sorted entries k BLK + t,
+    so the 64 lanes of a gather instruction take 64 consecutive sorted items,
+    and stores x[col] at x_lds[slot]; each lane finally reads its own slots
+    back and sums exactly as the flat probe does (same products, same order,
+    same bits)."""
+    from .codegen import _HIP_PRELUDE
+    ch = blk * u
+    if ch > 8192 or nb != blk or blk % 64 or u % 2:
+        raise ValueError("lsort probe: BLK x U <= 8192, NB == BLK, even U")
+    waves = blk // 64
+    L = [_HIP_PRELUDE,
+         'extern "C" __global__ __launch_bounds__(%d)' % blk,
+         "void %s(const tg_i64* __restrict__ indices, const double* __restrict__ data," % name,
+         "        const double* __restrict__ x, double* __restrict__ out, const tg_i64 nnz,",
+         "        const int shift) {",
+         "  __shared__ unsigned s_hist[%d];" % nb,
+         "  __shared__ unsigned long long s_ent[%d];" % ch,
+         "  __shared__ double s_x[%d];" % ch,
+         "  __shared__ unsigned s_wsum[%d];" % waves,
+         "  const tg_i64 p0 = (tg_i64)blockIdx.x * %d;" % ch,
+         "  const int cnt = (int)(nnz - p0 < %d ? nnz - p0 : %d);" % (ch, ch),
+         "  const int t = threadIdx.x, l = t & 63, wv = t >> 6;",
+         "  s_hist[t] = 0u;",
+         "  tg_i64 ci[%d]; double cv[%d];" % (u, u)]
+    for k in range(u // 2):
+        L += ["  {",
+              "    const int q = 2 * (%d + t);" % (k * blk),
+              "    if (q + 1 < cnt) {",
+              "      const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + p0 + q));",
+              "      const tg_f64x2 b = __builtin_nontemporal_load((const tg_f64x2*)(data + p0 + q));",
+              "      ci[%d] = a.x; ci[%d] = a.y; cv[%d] = b.x; cv[%d] = b.y;" % (2 * k, 2 * k + 1,
+                                                                          2 * k, 2 * k + 1),
+              "    } else {",
+              "      ci[%d] = q < cnt ? indices[p0 + q] : 0;" % (2 * k),
+              "      cv[%d] = q < cnt ? data[p0 + q] : 0.0;" % (2 * k),
+              "      ci[%d] = 0; cv[%d] = 0.0;" % (2 * k + 1, 2 * k + 1),
+              "    }",
+              "  }"]
+    L += ["  __syncthreads();",
+          "  // each item's rank in its bucket",
+          "  unsigned rk[%d]; int key[%d];" % (u, u)]
+    for j in range(u):
+        q = "2 * (%d + t) + %d" % ((j // 2) * blk, j % 2)
+        L.append("  { const int q = %s; key[%d] = (int)(ci[%d] >> shift); "
+                 "rk[%d] = q < cnt ? atomicAdd(&s_hist[key[%d]], 1u) : 0u; }" % (q, j, j, j, j))
+    L += ["  __syncthreads();",
+          "  // exclusive scan of the buckets: wave scans, then the waves' totals",
+          "  {",
+          "    const unsigned h = s_hist[t];",
+          "    unsigned v = h;",
+          "    #pragma unroll",
+          "    for (int d = 1; d < 64; d <<= 1) { const unsigned o = __shfl_up(v, d); if (l >= d) v += o; }",
+          "    if (l == 63) s_wsum[wv] = v;",
+          "    __syncthreads();",
+          "    unsigned base = 0;",
+          "    for (int w = 0; w < wv; ++w) base += s_wsum[w];",
+          "    s_hist[t] = base + v - h;",
+          "  }",
+          "  __syncthreads();"]
+    for j in range(u):
+        q = "2 * (%d + t) + %d" % ((j // 2) * blk, j % 2)
+        L.append("  { const int q = %s; if (q < cnt) s_ent[s_hist[key[%d]] + rk[%d]] = "
+                 "((unsigned long long)ci[%d] << 13) | (unsigned)(%d + t); }"
+                 % (q, j, j, j, j * blk))
+    L += ["  __syncthreads();",
+          "  // gathers in sorted order: 64 consecutive sorted items per instruction"]
+    for k in range(u):
+        L.append("  { const int s = %d + t; if (s < cnt) { const unsigned long long e = s_ent[s]; "
+                 "s_x[e & 8191u] = x[e >> 13]; } }" % (k * blk))
+    L += ["  __syncthreads();",
+          "  double acc = 0.0;"]
+    for j in range(u):
+        q = "2 * (%d + t) + %d" % ((j // 2) * blk, j % 2)
+        L.append("  { const int q = %s; acc += cv[%d] * (q < cnt ? s_x[%d + t] : 0.0); }"
+                 % (q, j, j * blk))
+    L += ["  acc = tg_segsum<%d>(acc);" % seg,
+          "  if (t %% %d == 0) out[((tg_i64)blockIdx.x * %d + t) / %d] = acc;" % (seg, blk, seg),
+          "}"]
+    return "\n".join(L) + "\n"
 
 
 def _slot_of_sorted(blk: int, u: int) -> np.ndarray:
@@ -210,20 +301,37 @@ def _shapes(text: str) -> List[Tuple[int, int]]:
 def _variants(orders: Sequence[str], shapes: Sequence[Tuple[int, int]],
               gathers: Sequence[str], seg: int) -> List[Tuple[str, str, int, int, str]]:
     """(kernel name, order, blk, u, gather); every order has a kernel of its
-    own name, so a rocprofv3 run tells them apart."""
+    own name, so a rocprofv3 run tells them apart.  Order ``lsort`` is the
+    matrix layout sorted by the workgroup itself (``lsort_source``)."""
     out = []
     for blk, u in shapes:
         for g in gathers:
             for o in (orders if g == "x" else ("matrix",)):
+                if o == "lsort" and (blk * u > 8192 or u % 2):
+                    continue
                 out.append(("probe_flat_%s_%s_b%du%d" % (g, o, blk, u), o, blk, u, g))
     return out
 
 
-def build(orders=("matrix", "b9", "line"), shapes=((1024, 4), (1024, 8), (512, 8)),
+def _source(name: str, order: str, blk: int, u: int, seg: int, g: str) -> str:
+    if order == "lsort":
+        return lsort_source(name, blk, u, seg, blk)
+    return flat_source(name, blk, u, seg, g)
+
+
+def lsort_shift(N: int, nb: int) -> int:
+    """The smallest shift that maps columns 0..N-1 onto fewer than nb buckets."""
+    s = 0
+    while ((max(N, 1) - 1) >> s) >= nb:
+        s += 1
+    return s
+
+
+def build(orders=("matrix", "b9", "line", "lsort"), shapes=((1024, 4), (1024, 8), (512, 8)),
           gathers=("x", "none", "one"), seg: int = 4) -> int:
     n = 0
-    for name, _o, blk, u, g in _variants(orders, shapes, gathers, seg):
-        _code_object(name, flat_source(name, blk, u, seg, g))
+    for name, o, blk, u, g in _variants(orders, shapes, gathers, seg):
+        _code_object(name, _source(name, o, blk, u, seg, g))
         n += 1
     return n
 
@@ -277,15 +385,17 @@ def run_flat(case_id: str, orders: Sequence[str], shapes: Sequence[Tuple[int, in
         for name, order, blk, u, g in variants:
             key = (order, blk, u)
             if key not in layouts:
-                ind, val = flat_layout(ind0, val0, blk, u, order)
+                ind, val = flat_layout(ind0, val0, blk, u,
+                                       "matrix" if order == "lsort" else order)
                 dev = [(rt.DeviceBuffer(ind), rt.DeviceBuffer(val)) for _ in range(copies)]
                 layouts[key] = (dev, ind, val, gather_lines(ind, blk, u))
             dev, ind, val, lpg = layouts[key]
-            fn = _function(name, flat_source(name, blk, u, seg, g))
+            fn = _function(name, _source(name, order, blk, u, seg, g))
             ch = blk * u
             grid = -(-nnz // ch)
             out = rt.DeviceBuffer(nbytes=grid * (blk // seg) * 8)
-            sets = [[dev[c][0], dev[c][1], xs[c], out, nnz] for c in range(copies)]
+            extra = [lsort_shift(N, blk)] if order == "lsort" else []
+            sets = [[dev[c][0], dev[c][1], xs[c], out, nnz] + extra for c in range(copies)]
             kms, _ = rt.time_launches(fn, grid, blk, 0, sets, warmup, iters)
             got = out.to_host(np.empty(grid * (blk // seg)))
             exp = flat_expected(ind, val, x, blk, u, seg, g)
@@ -313,7 +423,8 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
     ap.add_argument("probe", nargs="?", choices=["flat"], default="flat")
     ap.add_argument("--build", action="store_true", help="compile the probes and exit")
     ap.add_argument("--case", default="c1")
-    ap.add_argument("--order", default="matrix,b9,line")
+    ap.add_argument("--order", default="matrix,b9,line",
+                    help="matrix, line, b<shift> (host-sorted) or lsort (sorted in LDS)")
     ap.add_argument("--shape", default="1024x4,1024x8,512x8",
                     help="BLOCKxU per probe (U nonzeros per lane, even)")
     ap.add_argument("--gather", default="x,none,one")
@@ -327,7 +438,7 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
     args = ap.parse_args(argv)
     orders = [o for o in args.order.split(",") if o]
     for o in orders:
-        if o not in ("matrix", "line") and not (o[0] == "b" and o[1:].isdigit()):
+        if o not in ("matrix", "line", "lsort") and not (o[0] == "b" and o[1:].isdigit()):
             raise SystemExit("bad order %r (matrix, line or b<shift>)" % o)
     shapes = _shapes(args.shape)
     gathers = [g for g in args.gather.split(",") if g]

@@ -130,7 +130,22 @@ STREAM_TEST_SCHEDULES: List[Config] = [
 ]
 
 
+# Row tiles whose first-step gathers are sorted in LDS (gather "sorted"): one to
+# eight rows per lane group, odd and even unroll, lane groups of 1 to 64 lanes,
+# blocks of 1, 3, 8 and 16 waves (64 to 1024 buckets), 384 to 8192 sorted items.
+SORTED_TEST_SCHEDULES: List[Config] = [
+    Config(tile_size=256, threads_per_row=8, unroll=2, block_size=512, gather="sorted"),
+    Config(tile_size=64, threads_per_row=4, unroll=2, block_size=256, gather="sorted"),
+    Config(tile_size=128, threads_per_row=1, unroll=1, block_size=64, gather="sorted"),
+    Config(tile_size=32, threads_per_row=16, unroll=3, block_size=256, gather="sorted"),
+    Config(tile_size=8, threads_per_row=64, unroll=8, block_size=512, gather="sorted"),
+    Config(tile_size=24, threads_per_row=8, unroll=2, block_size=192, gather="sorted"),
+    Config(tile_size=512, threads_per_row=8, unroll=2, block_size=1024, gather="sorted"),
+]
+
+
 def schedule_id(c: Config) -> str:
-    return "T%d-TPR%d-U%d-V%d-B%d%s" % (c.tile_size, c.threads_per_row, c.unroll,
-                                        c.vector_width, c.block_size,
-                                        "" if c.balance == "rows" else "-" + c.balance)
+    return "T%d-TPR%d-U%d-V%d-B%d%s%s" % (c.tile_size, c.threads_per_row, c.unroll,
+                                          c.vector_width, c.block_size,
+                                          "" if c.balance == "rows" else "-" + c.balance,
+                                          "" if c.gather == "direct" else "-" + c.gather)
