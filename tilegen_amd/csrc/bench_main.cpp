@@ -286,6 +286,7 @@ int main(int argc, char** argv) {
 
   // GPU time of the dispatch itself
   std::vector<float> kms;
+  double enqueue_async_us = -1.0, enqueue_raw_us = -1.0;
   if (hip) {
     using Fn = void* (*)(void);
     using Fg = int (*)(int64_t, int64_t, int64_t, int64_t, int64_t*, int32_t*, int32_t*);
@@ -320,6 +321,36 @@ int main(int argc, char** argv) {
           std::fprintf(stderr, "error: %s\n", tg_last_error());
           return 4;
         }
+        // host cost of enqueueing one launch: a.iters back-to-back launches through
+        // the variant's tgv_launch_async (the product path: ordered launches for
+        // variants with module scratch) and through tg_run_launches (the raw
+        // dispatch), host clock around the enqueue loop only
+        if (kn == "spmv") {
+          using Fa = int (*)(void*, const int64_t*, const int64_t*, const double*, const double*,
+                             double*, int64_t, int64_t, int64_t);
+          Fa async = reinterpret_cast<Fa>(dlsym(h, "tgv_launch_async"));
+          if (async) {
+            tg_synchronize();
+            double t0 = now_ms();
+            for (int i = 0; i < a.iters; ++i) {
+              const Set& s = sets[i % sets.size()];
+              if (async(nullptr, s.ip, s.ind, s.dat, s.d0, s.o, M, N, nnz) != 0) {
+                std::fprintf(stderr, "error: tgv_launch_async: %s\n", tg_last_error());
+                return 4;
+              }
+            }
+            enqueue_async_us = (now_ms() - t0) * 1e3 / a.iters;
+            tg_synchronize();
+            t0 = now_ms();
+            if (tg_run_launches(kfn, grid, block, lds, slots.data(), nargs,
+                                static_cast<int>(sets.size()), a.iters, nullptr) != 0) {
+              std::fprintf(stderr, "error: %s\n", tg_last_error());
+              return 4;
+            }
+            enqueue_raw_us = (now_ms() - t0) * 1e3 / a.iters;
+            tg_synchronize();
+          }
+        }
       }
     }
   }
@@ -347,12 +378,14 @@ int main(int argc, char** argv) {
       "{\"kernel\":\"%s\",\"config\":%s,\"backend\":\"%s\",\"matrix\":\"%s\",\"rows\":%lld,"
       "\"cols\":%lld,\"nnz\":%lld,\"K\":%lld,\"ms_mean\":%.6g,\"ms_min\":%.6g,"
       "\"gflops\":%.6g,\"bandwidth_gbs\":%.6g,\"max_abs_err\":%.6g,\"max_rel_err\":%.6g,"
-      "\"timer\":\"%s\",\"launch_wall_ms_mean\":%.6g,\"rotate\":%d}\n",
+      "\"timer\":\"%s\",\"launch_wall_ms_mean\":%.6g,\"rotate\":%d,"
+      "\"enqueue_us_async\":%.4g,\"enqueue_us_raw\":%.4g}\n",
       escape(kn).c_str(), a.config.c_str(), escape(a.backend).c_str(), escape(a.matrix).c_str(),
       (long long)M, (long long)N, (long long)nnz, (long long)(kn == "spmv" ? 0 : K), mean, mn,
       mn > 0 ? flops / (mn * 1e6) : 0.0, mn > 0 ? bytes_ref / (mn * 1e6) : 0.0, max_abs, max_rel,
       kms.empty() ? "host clock around launch" : "dispatch events (tg_time_launches)",
-      wall.empty() ? 0.0 : wsum / wall.size(), hip ? a.rotate : 1);
+      wall.empty() ? 0.0 : wsum / wall.size(), hip ? a.rotate : 1, enqueue_async_us,
+      enqueue_raw_us);
   for (void* p : owned) tg_free(p);
   // no dlclose: an OpenMP variant's worker threads still run code from it; the
   // library goes away with the process
