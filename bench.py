@@ -364,7 +364,10 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
-    ap.add_argument("--warmup", type=int, default=40)
+    # untimed launches before each timed loop; 2000 of c1 are about 25 ms of
+    # back-to-back work (after 40, the event-timed average of c1's tuned
+    # schedule read 12.9 us against 12.4 us after 4000, its median 12.5 in both)
+    ap.add_argument("--warmup", type=int, default=2000)
     ap.add_argument("--case", default=None,
                     help="run this BASELINE config alone (default: c1 as the headline plus "
                          "every other config under 'cases')")

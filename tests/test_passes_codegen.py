@@ -495,7 +495,9 @@ def test_lane_group_rows_load_before_any_gather():
     # the loads sit in the per-lane guarded block, the gathers do not
     assert src.count("if (q < re[r] && rs[r] < re[r])", loads, guard) == 1
     assert "if (q < re[r]" not in src[guard:sums]
-    one = generate(standard_kernels()["spmv"], TUNED["c1"], "hip", write=False).source
+    one = generate(standard_kernels()["spmv"],
+                   Config(tile_size=16, threads_per_row=8, unroll=2, block_size=128), "hip",
+                   write=False).source
     assert "every row's loads" not in one
     assert "// first step of every row in flight before any accumulation" in one
     # past R U = 8 the operands of every row would not fit in registers: one step per row

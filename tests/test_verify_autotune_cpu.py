@@ -172,3 +172,22 @@ def test_bench_openmp_leg_on_cpu():
     assert r["kind"] == "openmp backend" and r["schedule"] == BASELINE.short()
     assert r["rel_err"] <= 1e-12 and r["cores"] >= 1 and r["value"] > 0
     assert "-fopenmp" in r["compile"]
+
+
+@pytest.mark.parametrize("kernel", ["spmv", "fused_spmv_axpy"])
+def test_sorted_space_matches_the_emitter(kernel):
+    """Row tiles with sorted first-step gathers are in the SpMV search space
+    exactly where the emitter accepts them: every legal one generates, every one
+    pruned for the sort's limits is refused by the emitter too."""
+    from tilegen_amd.schedules import TUNED
+    sorted_ = [(c, r) for c, r in enumerate_configs(kernel) if c.gather == "sorted"]
+    legal = [c for c, r in sorted_ if r is None]
+    limited = [c for c, r in sorted_ if r is not None and r.startswith("sorted")]
+    assert len(legal) > 100 and limited
+    k = standard_kernels()[kernel]
+    for c in legal:
+        generate(k, c, "hip", write=False)
+    for c in limited:
+        with pytest.raises(ValueError, match="sorted"):
+            generate(k, c, "hip", write=False)
+    assert TUNED["c1"] in legal

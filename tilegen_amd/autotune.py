@@ -177,6 +177,9 @@ def enumerate_configs(kernel: Optional[str] = None, K: int = 8
         out += [(dataclasses.replace(c, balance="stream"),
                  r if r is not None else _stream_reason(c)) for c, r in rows
                 if c.tile_size == c.block_size // c.threads_per_row]
+        # and row tiles whose first-step gathers are sorted in LDS
+        out += [(dataclasses.replace(c, gather="sorted"),
+                 r if r is not None else _sorted_reason(c)) for c, r in rows]
     return out
 
 
@@ -186,6 +189,20 @@ def _stream_reason(cfg: Config) -> Optional[str]:
     if cfg.block_size * cfg.unroll > STREAM_MAX_CHUNK:
         return "stream range of %d nonzeros exceeds %d" % (cfg.block_size * cfg.unroll,
                                                           STREAM_MAX_CHUNK)
+    return None
+
+
+def _sorted_reason(cfg: Config) -> Optional[str]:
+    """A sorted tile holds its first step in registers (rows per lane group x
+    unroll <= 8) and its items in LDS (at most SORT_MAX_ITEMS)."""
+    from .codegen import SORT_MAX_ITEMS
+    slots = cfg.block_size // cfg.threads_per_row
+    rows = -(-cfg.tile_size // slots)
+    if rows * cfg.unroll > 8:
+        return "sorted first step of %d rows x unroll %d per lane exceeds 8" % (rows, cfg.unroll)
+    if rows * cfg.unroll * cfg.block_size > SORT_MAX_ITEMS:
+        return "sorted first step of %d items exceeds %d" % (
+            rows * cfg.unroll * cfg.block_size, SORT_MAX_ITEMS)
     return None
 
 

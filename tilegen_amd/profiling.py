@@ -45,7 +45,7 @@ __all__ = ["commands", "case_plan", "trace_rows", "pmc_rows", "summarize", "valu
 COPY_MIB = 256
 HEADLINE = "c1"
 CASE_ORDER = ("c1", "c2", "c3a", "c3b", "c4", "c5", "c5x25")
-STEPS, WARMUP, CASE_ITERS = 20, 5, 200
+STEPS, WARMUP, CASE_ITERS = 100, 2000, 200
 PMC_CASE_ITERS = 20
 BENCH_TRACE = "python3 bench.py --steps %d --warmup %d" % (STEPS, WARMUP)
 BENCH_PMC = "python3 bench.py --no-cpu --steps %d --warmup %d --case-iters %d" % (

@@ -15,9 +15,15 @@ from .codegen import Config
 TUNED: Dict[str, Config] = {
     # winners of an exhaustive sweep of the legal CDNA4 space on one MI355X,
     # cold (rotated) inputs, GPU-event kernel time
-    # 16 nonzeros per row: 8 lanes x 2 consecutive nonzeros (one 128-bit load of
-    # indices and one of values per lane), 8 rows per wave
-    "c1": Config(tile_size=16, threads_per_row=8, unroll=2, vector_width=1, block_size=128),
+    # 16 nonzeros per row, uniform random columns: tiles of 256 rows on 4-lane
+    # groups x 4 nonzeros (two row passes per group: every nonzero of the tile
+    # is one first-step item), the tile's 4096 gathers sorted by column in LDS
+    # so that each gather instruction's 64 lanes share cache lines of x;
+    # 12.3-12.4 us against 12.6 for the best direct-gather tiles
+    # (T16/TPR8/U2/B128) and 15.8 for the same tiles with direct gathers
+    # (interleaved repeats on one box)
+    "c1": Config(tile_size=256, threads_per_row=4, unroll=4, vector_width=1, block_size=512,
+                 gather="sorted"),
     # 7 nonzeros per row: 4 lanes x 2
     "c2": Config(tile_size=128, threads_per_row=4, unroll=2, vector_width=1, block_size=256),
     # skewed rows, stream ranges: every workgroup takes an equal range of B x U
