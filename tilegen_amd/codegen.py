@@ -1679,6 +1679,7 @@ __device__ tg_i64 tg_st_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 
 
 
 SORT_MAX_ITEMS = 8192   # slots of a sorted tile's first step (13 bits in an LDS entry)
+SORT_ZPAD = 1024        # zeros read by a sorted tile's guessed loads without a guess (>= 64 x 8 + 2)
 
 
 def sort_buckets(block: int) -> int:
@@ -1999,6 +2000,18 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
               " : 0;" % (NB, NB.bit_length() - 1))
             w("if (threadIdx.x < %d) s_hist[threadIdx.x] = 0u;" % NB)
         if sorted_:
+            # the row pointers' first pass goes out first: vector loads return in order, so
+            # issued after the guessed loads, their staging would wait for all of those too
+            w("// the first %d row pointers, loaded before anything else (a relaxed atomic load," % min(TR + 1, B))
+            w("// which the compiler issues here rather than at its use below)")
+            w("tg_i64 ptr0_ = 0;")
+            w.open("if (threadIdx.x <= %d)" % TR)
+            w("const tg_i64 r = row0 + threadIdx.x;")
+            w("typedef const __attribute__((address_space(1))) tg_i64 tg_gi64;")
+            w("ptr0_ = __hip_atomic_load((tg_gi64*)indptr + (r < row_end ? r : row_end), "
+              "__ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);")
+            w.close()
+        if sorted_:
             w("// Before the row pointers, each row's first step is loaded where rows of Ls =")
             w("// nnz / M nonzeros each from position 0 would put it, when nnz is such a multiple")
             w("// of M that every lane's 128-bit pairs lie inside its row (positions below nnz,")
@@ -2018,23 +2031,34 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
             w("gs[r] = lr < %d && grow < row_end ? grow * Ls : -1;" % TR)
             w.close()
             if U % 2 == 0:
-                w.open("if (Ls > 0)")
+                if pre is None:
+                    raise ValueError("gather 'sorted' needs file-scope declarations")
+                pre("// zeros that a sorted tile's guessed loads read when there is no guess, so\n"
+                    "// that those loads are issued unconditionally (never written)\n"
+                    "__device__ __attribute__((aligned(16))) tg_i64 tg_zpad[%d];" % SORT_ZPAD)
+                w("// without a guess the same loads read zeros, so that no branch separates them")
+                w("// from the row pointers' load: their staging then waits for that load alone")
+                w("const tg_i64* const sidx_ = Ls > 0 ? indices : (const tg_i64*)tg_zpad;")
+                w("const double* const sdat_ = Ls > 0 ? data : (const double*)tg_zpad;")
                 w("#pragma unroll")
                 w.open("for (int r = 0; r < %d; ++r)" % R)
-                w("const tg_i64 gb = gs[r] >= 0 ? gs[r] : 0;")
+                w("const tg_i64 gb = Ls > 0 && gs[r] >= 0 ? gs[r] : 0;")
                 for u in range(0, U, 2):
                     w("{ const tg_i64 q = %s;" % fpos("gb", u))
-                    w("  const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + q));"
+                    w("  const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(sidx_ + q));"
                       " fci[r][%d] = a.x; fci[r][%d] = a.y;" % (u, u + 1))
-                    w("  const tg_f64x2 b = __builtin_nontemporal_load((const tg_f64x2*)(data + q));"
+                    w("  const tg_f64x2 b = __builtin_nontemporal_load((const tg_f64x2*)(sdat_ + q));"
                       " fcv[r][%d] = b.x; fcv[r][%d] = b.y; }" % (u, u + 1))
                 w.close()
-                w.close()
         w("if (threadIdx.x == 0) { s_nlong = 0;%s }" % (" s_nmed = 0;" if wave_tier else ""))
-        w.open("for (int t = threadIdx.x; t <= %d; t += %d)" % (TR, B))
-        w("const tg_i64 r = row0 + t;")
-        w("s_ptr[t] = indptr[r < row_end ? r : row_end];")
-        w.close()
+        if sorted_:
+            w("if (threadIdx.x <= %d) s_ptr[threadIdx.x] = ptr0_;" % TR)
+        if not sorted_ or TR + 1 > B:
+            w.open("for (int t = threadIdx.x%s; t <= %d; t += %d)" % (" + %d" % B if sorted_ else "",
+                                                                      TR, B))
+            w("const tg_i64 r = row0 + t;")
+            w("s_ptr[t] = indptr[r < row_end ? r : row_end];")
+            w.close()
         if hybrid:
             w("// indptr[0] and indptr[M] with the row pointers: which long rows have ranges")
             w("__shared__ tg_i64 s_lim[2];")
