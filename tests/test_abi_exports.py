@@ -233,6 +233,29 @@ def test_tuned_schedules_do_not_spill(tmp_path):
         assert all(v == "0" for v in meta.values()), (label, cfg.short(), meta)
 
 
+def test_noalloc_library_code_object_does_not_spill(tmp_path):
+    """libtgna's own kernels, compiled by hipcc with the library's flags (not the
+    hipRTC build of the same schedule above), keep every value in registers."""
+    readelf = "/opt/rocm/llvm/bin/llvm-readelf"
+    if not os.path.exists(readelf):
+        pytest.skip("llvm-readelf not available")
+    from tilegen_amd.build import noalloc_code_object
+    co = noalloc_code_object(str(tmp_path / "libtgna_device.co"))
+    notes = subprocess.run([readelf, "--notes", co], capture_output=True, text=True).stdout
+    kernels = re.split(r"\n\s+- \.", notes)
+    found = {}
+    for k in kernels:
+        name = re.search(r"\.name:\s+(\S+)", k)
+        if not name:
+            continue
+        meta = dict(re.findall(r"\.(private_segment_fixed_size|vgpr_spill_count|"
+                               r"sgpr_spill_count):\s+(\d+)", k))
+        found[name.group(1)] = meta
+    assert "spmv_kernel" in found and any("tg_na_clear" in n for n in found), sorted(found)
+    for name, meta in found.items():
+        assert len(meta) == 3 and all(v == "0" for v in meta.values()), (name, meta)
+
+
 def test_noalloc_library_exports_its_header():
     """libtgna.so exports exactly what include/tilegen_noalloc.h declares and
     loads without a GPU."""
