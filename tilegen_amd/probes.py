@@ -35,6 +35,12 @@ kept and its line traffic removed).
     python -m tilegen_amd.probes flat --case c1 --order matrix,b9,line \\
         --shape 1024x4,1024x8 [--gather x,none,one] [--json out.json]
     python -m tilegen_amd.probes --build          # compile every probe (no GPU)
+
+``placement`` launches workgroups of a kernel's footprint (block, static LDS) at
+several grid sizes and reports how many CUs took them and how many took two or
+more (``run_placement``):
+
+    python -m tilegen_amd.probes placement --grids 194,239,256 --block 1024 --lds 45264
 """
 
 from __future__ import annotations
@@ -290,6 +296,72 @@ def _function(name: str, src: str) -> int:
     return int(fn.value)
 
 
+def placement_source(name: str, blk: int, lds_bytes: int, spin_ticks: int) -> str:
+    """``placement``: where the dispatcher puts the workgroups of a grid.  Each
+    workgroup of ``blk`` lanes and ``lds_bytes`` of static LDS (the footprint of the
+    kernel whose placement is in question) records its XCC and hardware id
+    (``HW_REG_XCC_ID``, ``HW_REG_HW_ID``: SIMD, CU, shader array and engine) and its
+    start time, then stays resident for ``spin_ticks`` of the 100 MHz real-time
+    clock (at most 2^22 polls), so that the whole grid is resident at once."""
+    return "\n".join([
+        "typedef unsigned long long u64;",
+        'extern "C" __global__ __launch_bounds__(%d)' % blk,
+        "void %s(u64* __restrict__ rec, const int pad_index) {" % name,
+        "  __shared__ unsigned char s_pad[%d];" % lds_bytes,
+        "  unsigned hw, xcc;",
+        '  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));',
+        '  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));',
+        "  const u64 t0 = __builtin_amdgcn_s_memrealtime();",
+        "  // keep the LDS allocation: one byte written, read back after the barrier",
+        "  if (threadIdx.x == 0) s_pad[pad_index] = 1;",
+        "  __syncthreads();",
+        "  #pragma unroll 1",
+        "  for (int i = 0; i < (1 << 22); ++i)",
+        "    if (__builtin_amdgcn_s_memrealtime() - t0 >= %dull) break;" % spin_ticks,
+        "  if (threadIdx.x == 0) {",
+        "    rec[3 * blockIdx.x] = ((u64)(xcc & 0xffffu) << 32) | hw;",
+        "    rec[3 * blockIdx.x + 1] = t0;",
+        "    rec[3 * blockIdx.x + 2] = s_pad[pad_index];",
+        "  }",
+        "}",
+        ""])
+
+
+def placement_cu(rec_word: int) -> Tuple[int, int]:
+    """(XCC, CU key) of a placement record: the HW_ID bits above the wave's SIMD and
+    slot (CU, shader array, shader engine, bits 8-15)."""
+    return int(rec_word >> 32) & 0xF, (int(rec_word) >> 8) & 0xFF
+
+
+def run_placement(grids: Sequence[int], blk: int, lds_bytes: int,
+                  spin_ticks: int = 2000) -> List[dict]:
+    """Launch the placement probe at each grid size; per grid, how many CUs took
+    workgroups and how many took more than one."""
+    from . import runtime as rt
+    name = "probe_placement_b%d_l%d" % (blk, lds_bytes)
+    fn = _function(name, placement_source(name, blk, lds_bytes, spin_ticks))
+    out = []
+    for g in grids:
+        buf = rt.DeviceBuffer(np.zeros(3 * g, dtype=np.uint64))
+        pad = np.int32(lds_bytes - 1)
+        rt.launch(fn, g, blk, 0, [buf, pad])
+        rt.synchronize()
+        rec = buf.to_host().view(np.uint64).reshape(g, 3)
+        buf.free()
+        cus = {}
+        for b in range(g):
+            cus.setdefault(placement_cu(int(rec[b, 0])), []).append(b)
+        per = np.bincount([len(v) for v in cus.values()])
+        xcc_of = [placement_cu(int(rec[b, 0]))[0] for b in range(g)]
+        out.append({"grid": g, "block": blk, "lds_bytes": lds_bytes, "cus": len(cus),
+                    "max_per_cu": int(max(len(v) for v in cus.values())),
+                    "cus_with_2_or_more": int(sum(per[2:])) if len(per) > 2 else 0,
+                    "xcc_is_block_mod_8": all(xcc_of[b] == b % 8 for b in range(g)),
+                    "all_loaded_pad": bool(np.all(rec[:, 2] == 1)),
+                    "start_spread_us": float((rec[:, 1].max() - rec[:, 1].min()) / 100.0)})
+    return out
+
+
 def _shapes(text: str) -> List[Tuple[int, int]]:
     out = []
     for part in text.split(","):
@@ -420,7 +492,11 @@ def run_flat(case_id: str, orders: Sequence[str], shapes: Sequence[Tuple[int, in
 
 def main(argv: Optional[Sequence[str]] = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("probe", nargs="?", choices=["flat"], default="flat")
+    ap.add_argument("probe", nargs="?", choices=["flat", "placement"], default="flat")
+    ap.add_argument("--grids", default="194,207,222,239,250,256,259",
+                    help="placement: grid sizes")
+    ap.add_argument("--block", type=int, default=1024, help="placement: workgroup size")
+    ap.add_argument("--lds", type=int, default=45264, help="placement: static LDS bytes")
     ap.add_argument("--build", action="store_true", help="compile the probes and exit")
     ap.add_argument("--case", default="c1")
     ap.add_argument("--order", default="matrix,b9,line",
@@ -445,10 +521,18 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
     if args.build:
         t0 = time.time()
         n = build(orders, shapes, gathers, args.seg)
+        for blk, lds in ((1024, 45264), (512, 28816)):
+            nm = "probe_placement_b%d_l%d" % (blk, lds)
+            _code_object(nm, placement_source(nm, blk, lds, 2000))
+            n += 1
         print("built %d probe code objects in %.1fs" % (n, time.time() - t0))
         return 0
-    recs = run_flat(args.case, orders, shapes, gathers, args.seg, args.warmup, args.iters,
-                    args.repeats, not args.no_control)
+    if args.probe == "placement":
+        grids = [int(g) for g in args.grids.split(",") if g]
+        recs = run_placement(grids, args.block, args.lds)
+    else:
+        recs = run_flat(args.case, orders, shapes, gathers, args.seg, args.warmup, args.iters,
+                        args.repeats, not args.no_control)
     for r in recs:
         print(json.dumps(r, separators=(",", ":")), flush=True)
     if args.json:
