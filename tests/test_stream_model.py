@@ -42,6 +42,7 @@ import pytest
 from tilegen_amd import codegen as cg
 from tilegen_amd.codegen import Config, generate
 from tilegen_amd.dsl import standard_kernels
+from tilegen_amd.schedules import TUNED
 
 
 def _row_holding(indptr, p):
@@ -247,3 +248,27 @@ def test_stream_schedule_checks():
         generate(standard_kernels()["spmm"],
                  Config(tile_size=64, threads_per_row=4, unroll=2, block_size=256,
                         balance="stream"), "hip", write=False)
+
+
+def test_common_case_copy_has_no_general_case_code():
+    """Phases 2-4 come twice: under indptr[0] = 0 and indptr[M] = nnz every range's
+    staged positions end where its owned ones do (the model above: p1 == ps for every
+    range when nnz is exact and the matrix starts at position 0), so that copy has no
+    tail loads, no clamp of ranges past the grid and no partly-staged test; the copy for
+    every other case keeps all three."""
+    src = generate(standard_kernels()["spmv"], TUNED["c3a"], "hip", write=False).source
+    body = src[src.index("__global__"):]
+    i = body.index("if (pbase == 0 && pend == nnz) {")
+    j = body.index("else {", i)
+    fast, general = body[i:j], body[j:]
+    assert "if (ps < p1)" not in fast and "NL - 1 ?" not in fast and "en <= qhi" not in fast
+    assert general.count("if (ps < p1)") == 2 and "NL - 1 ?" in general and "en <= qhi" in general
+    for M, nnz, CH in ((100, 4096 * 3 + 17, 4096), (7, 4096 * 2, 4096), (5, 0, 2048)):
+        grid = nnz // CH + 1
+        NR = (nnz + CH - 1) // CH if nnz > 0 else 1
+        NL = min(NR, grid)
+        for e in range(NL):
+            pa = e * CH
+            ps = min(pa + CH, nnz)
+            p1 = nnz if e == NL - 1 else ps
+            assert p1 == ps

@@ -1415,10 +1415,12 @@ def _hip_stream_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         """One wave adds the row's positions [lo, hi) past the staged ones, with its
         own loads (only the grid's last range, when nnz undercounts the rows'
         nonzeros, has any)."""
+        w.open("if (ps < p1)")  # uniform: false unless nnz undercounts
         w("#pragma unroll 1")
         w.open("for (tg_i64 pq = (%s) + l; pq < (%s); pq += 64)" % (lo, hi))
         w("const tg_i64 cq = indices[pq];")
         w("%s += %s;" % (acc, _value_with(plan, "data[pq]", gather("cq"), row, "cq")))
+        w.close()
         w.close()
 
     _merge_decls(pre, scratch_arg)
@@ -1473,35 +1475,37 @@ __device__ tg_i64 tg_st_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 
     def phase1(positions: bool) -> None:
         """Stage the range's products and find its bounding rows, for positions
         pa + q, q in [qlo, qhi), and the rows holding P0 and P1 among the
-        nonzeros [sb, se); with ``positions``, also load indptr[0] and
-        indptr[M] once the range's own loads are issued."""
+        nonzeros [sb, se); with ``positions`` (the first run, whose qlo is 0),
+        also load indptr[0] and indptr[M] once the range's own loads are issued."""
+        def inr(q: str) -> str:
+            # staged position q; the first run's qlo is 0, which q never falls below
+            return "(%s < qhi)" % q if positions else "((%s >= qlo) & (%s < qhi))" % (q, q)
+
         w("// 1. this range's indices and values, every load issued before any is used")
         w("tg_i64 ci[%d]; double cv[%d];" % (U, U))
         if U % 2 == 0:
             for u in range(0, U, 2):
                 w.open("")
                 w("const int q = %s;" % pos(u))
-                w.open("if (pair_ok && q >= qlo && q + 1 < qhi)")
+                w.open("if (pair_ok && %sq + 1 < qhi)" % ("" if positions else "q >= qlo && "))
                 w("const tg_i64x2 a = __builtin_nontemporal_load((const tg_i64x2*)(indices + pa + q));")
                 w("const tg_f64x2 b = __builtin_nontemporal_load((const tg_f64x2*)(data + pa + q));")
                 w("ci[%d] = a.x; ci[%d] = a.y; cv[%d] = b.x; cv[%d] = b.y;" % (u, u + 1, u, u + 1))
                 w.close()
                 w.open("else")
                 for d in (0, 1):
-                    w("ci[%d] = ((q + %d >= qlo) & (q + %d < qhi)) ? "
-                      "__builtin_nontemporal_load(indices + pa + q + %d) : 0;" % (u + d, d, d, d))
-                    w("cv[%d] = ((q + %d >= qlo) & (q + %d < qhi)) ? "
-                      "__builtin_nontemporal_load(data + pa + q + %d) : 0.0;" % (u + d, d, d, d))
+                    w("ci[%d] = %s ? __builtin_nontemporal_load(indices + pa + q + %d) : 0;"
+                      % (u + d, inr("q + %d" % d), d))
+                    w("cv[%d] = %s ? __builtin_nontemporal_load(data + pa + q + %d) : 0.0;"
+                      % (u + d, inr("q + %d" % d), d))
                 w.close()
                 w.close()
         else:
             for u in range(U):
                 w.open("")
                 w("const int q = %s;" % pos(u))
-                w("ci[%d] = ((q >= qlo) & (q < qhi)) ? __builtin_nontemporal_load(indices + pa + q) : 0;"
-                  % u)
-                w("cv[%d] = ((q >= qlo) & (q < qhi)) ? __builtin_nontemporal_load(data + pa + q) : 0.0;"
-                  % u)
+                w("ci[%d] = %s ? __builtin_nontemporal_load(indices + pa + q) : 0;" % (u, inr("q")))
+                w("cv[%d] = %s ? __builtin_nontemporal_load(data + pa + q) : 0.0;" % (u, inr("q")))
                 w.close()
         if positions:
             w("// wave 0 alone loads indptr[0] and indptr[M] (for the check after the barrier)")
@@ -1524,11 +1528,12 @@ __device__ tg_i64 tg_st_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 
         w("// the operands (positions past the range gather nothing) and the products, in LDS")
         w("double xv[%d];" % U)
         for u in range(U):
-            w("{ const int q = %s; xv[%d] = ((q >= qlo) & (q < qhi)) ? %s : 0.0; }"
-              % (pos(u), u, gather("ci[%d]" % u)))
+            w("{ const int q = %s; xv[%d] = %s ? %s : 0.0; }"
+              % (pos(u), u, inr("q"), gather("ci[%d]" % u)))
         for u in range(U):
-            w("{ const int q = %s; if ((q >= qlo) & (q < qhi)) s_prod[q] = %s; }"
-              % (pos(u), _value_with(plan, "cv[%d]" % u, "xv[%d]" % u, row, "ci[%d]" % u)))
+            w("{ const int q = %s; if %s s_prod[q] = %s; }"
+              % (pos(u), inr("q") if not positions else "(q < qhi)",
+                 _value_with(plan, "cv[%d]" % u, "xv[%d]" % u, row, "ci[%d]" % u)))
 
     w("// Phase 1 first runs on the launch's own numbers, as if indptr[0] = 0 and")
     w("// indptr[M] = nnz (the common case), so that its loads wait for nothing: range e")
@@ -1570,111 +1575,131 @@ __device__ tg_i64 tg_st_row(const tg_i64* __restrict__ indptr, tg_i64 R, tg_i64 
     phase1(False)
     w("__syncthreads();")
     w.close()
-    w("const tg_i64 ra = s_b[0], ra_s = s_b[1], ra_e = s_b[2];")
-    w("const tg_i64 rb = s_b[3], rb_s = s_b[4], rb_e = s_b[5];")
-    w("// row ra began in an earlier range, so this range holds its last piece")
-    w("const bool ra_cut = e > 0 && ra < rb && ra_s < p0;")
-    w("// 2. the pieces cut at range edges first, so that their atomics overlap the row sums")
-    w.open("if (wv == 0 && ra_cut)")
-    w("// the ranges it spans (ra ends in this range: it holds p0 and ends before rb)")
-    w("const tg_i64 ef = (ra_s - pal) / %d, el = e;" % CH)
-    w.open("if (el < %d)" % MERGE_CAP)
-    w("const int en = (int)(ra_e - pa);")
-    w("double t = 0.0;")
-    w("#pragma unroll 4")
-    w("for (int q = qlo + l; q < (en < qhi ? en : qhi); q += 64) t += s_prod[q];")
-    tail("ps > ra_s ? ps : ra_s", "ra_e", "t")
-    w("t = tg_segsum<64>(t);")
-    w("double tot = t;")
-    w.open("if (tg_mp_commit(tg_part, e, ef, el, t, &tot) && l == 0 && ra < row_end)")
-    store("tot", "ra")
+    def phases(general: bool) -> None:
+        """Phases 2-4 after the barrier.  Without ``general`` (indptr[0] = 0 and
+        indptr[M] = nnz: every range's staged positions end where its owned ones do)
+        there are no tail loads, no ranges past the grid and no partly staged rows."""
+        w("const tg_i64 ra = s_b[0], ra_s = s_b[1], ra_e = s_b[2];")
+        w("const tg_i64 rb = s_b[3], rb_s = s_b[4], rb_e = s_b[5];")
+        w("// row ra began in an earlier range, so this range holds its last piece")
+        w("const bool ra_cut = e > 0 && ra < rb && ra_s < p0;")
+        w("// 2. the pieces cut at range edges first, so that their atomics overlap the row sums")
+        w.open("if (wv == 0 && ra_cut)")
+        w("// the ranges it spans (ra ends in this range: it holds p0 and ends before rb)")
+        w("const tg_i64 ef = (ra_s - pal) / %d, el = e;" % CH)
+        w.open("if (el < %d)" % MERGE_CAP)
+        w("const int en = (int)(ra_e - pa);")
+        w("double t = 0.0;")
+        w("#pragma unroll 4")
+        w("for (int q = qlo + l; q < (en < qhi ? en : qhi); q += 64) t += s_prod[q];")
+        if general:
+            tail("ps > ra_s ? ps : ra_s", "ra_e", "t")
+        w("t = tg_segsum<64>(t);")
+        w("double tot = t;")
+        w.open("if (tg_mp_commit(tg_part, e, ef, el, t, &tot) && l == 0 && ra < row_end)")
+        store("tot", "ra")
+        w.close()
+        w.close()
+        w("// otherwise the range it begins in sums it whole (below)")
+        w.close()
+        w.open("if (wv == %d && rb < n_rows && rb_s < p1)" % (1 if WAVES > 1 else 0))
+        w("const tg_i64 ef = (rb_s - pal) / %d, el0 = (rb_e - 1 - pal) / %d;" % (CH, CH))
+        if general:
+            w("const tg_i64 el = el0 < NL - 1 ? el0 : NL - 1;  // ranges past the grid's last do not exist")
+        else:
+            w("const tg_i64 el = el0;")
+        w.open("if (el < %d)" % MERGE_CAP)
+        w("const int st = (int)((rb_s > p0 ? rb_s : p0) - pa);")
+        w("double t = 0.0;")
+        w("#pragma unroll 4")
+        w("for (int q = st + l; q < qhi; q += 64) t += s_prod[q];")
+        w("t = tg_segsum<64>(t);")
+        w("double tot = t;")
+        w.open("if (tg_mp_commit(tg_part, e, ef, el, t, &tot) && l == 0 && rb < row_end)")
+        store("tot", "rb")
+        w.close()
+        w.close()
+        w("// otherwise, when it begins here, this workgroup sums it whole (below)")
+        w.close()
+        w("// 3. the owned rows [ra, rb), %d row pointers at a time" % RB)
+        w("const int lane = threadIdx.x %% %d;" % TPR)
+        w("const int slot = threadIdx.x / %d;" % TPR)
+        w("#pragma unroll 1")
+        w.open("for (tg_i64 b0 = ra; b0 < rb; b0 += %d)" % RB)
+        w("const int nb = (int)(rb - b0 < %d ? rb - b0 : %d);" % (RB, RB))
+        w("for (int i = threadIdx.x; i <= nb; i += %d) s_ptr[i] = indptr[b0 + i];" % B)
+        w("__syncthreads();")
+        w("// rows of up to 64 nonzeros: one lane group each")
+        w("#pragma unroll 1")
+        w.open("for (int i = slot; i < nb; i += %d)" % SLOTS)
+        w("const tg_i64 rs = s_ptr[i], re = s_ptr[i + 1];")
+        w("const int st = (int)((rs > p0 ? rs : p0) - pa), en = (int)(re - pa);")
+        w("const bool mine = !(b0 + i == ra && ra_cut);  // a cut ra was committed above")
+        w("const bool own = mine && en - st <= 64%s;%s" % (
+            (" && en <= qhi", "  // staged whole") if general else ("", "")))
+        w("double acc = 0.0;")
+        w.open("if (own)")
+        w("#pragma unroll 4")
+        w("for (int q = st + lane; q < en; q += %d) acc += s_prod[q];" % TPR)
+        w.close()
+        w("if (mine && !own && lane == 0) s_long[atomicAdd(&s_nlong, 1)] = i;")
+        w("acc = tg_segsum<%d>(acc);" % TPR)
+        w.open("if (own && lane == 0 && b0 + i < row_end)")
+        store("acc", "b0 + i")
+        w.close()
+        w.close()
+        w("__syncthreads();")
+        w("// longer rows: one wave each")
+        w("const int nl = s_nlong;")
+        w("#pragma unroll 1")
+        w.open("for (int k = wv; k < nl; k += %d)" % WAVES)
+        w("const int i = s_long[k];")
+        w("const tg_i64 rs = s_ptr[i], re = s_ptr[i + 1];")
+        w("const int st = (int)((rs > p0 ? rs : p0) - pa), en = (int)(re - pa);")
+        w("double acc = 0.0;")
+        w("#pragma unroll 4")
+        w("for (int q = st + l; q < (en < qhi ? en : qhi); q += 64) acc += s_prod[q];")
+        if general:
+            tail("ps > rs ? ps : rs", "re", "acc")
+        w("acc = tg_segsum<64>(acc);")
+        w.open("if (l == 0 && b0 + i < row_end)")
+        store("acc", "b0 + i")
+        w.close()
+        w.close()
+        w("__syncthreads();  // every wave has read s_nlong, s_long and s_ptr")
+        w("if (threadIdx.x == 0) s_nlong = 0;")
+        w.close()
+        w("// 4. row rb, when it begins in this range and reaches past the scratch's last range:")
+        w("// summed whole by the whole workgroup with its own loads, the waves' sums added in")
+        w("// wave order (the condition is the same for every wave)")
+        last_range = ("((rb_e - 1 - pal) / %d < NL - 1 ? (rb_e - 1 - pal) / %d : NL - 1)" % (CH, CH)
+                      if general else "(rb_e - 1 - pal) / %d" % CH)
+        w.open("if (rb < n_rows && rb_s < p1 && (rb_s - pal) / %d == e && %s >= %d)"
+               % (CH, last_range, MERGE_CAP))
+        w("double t = 0.0;")
+        w("#pragma unroll 4")
+        w.open("for (tg_i64 pq = rb_s + (tg_i64)threadIdx.x; pq < rb_e; pq += %d)" % B)
+        w("const tg_i64 cq = indices[pq];")
+        w("t += %s;" % _value_with(plan, "data[pq]", gather("cq"), row, "cq"))
+        w.close()
+        w("t = tg_segsum<64>(t);")
+        w("if (l == 0) s_wsum[wv] = t;")
+        w("__syncthreads();")
+        w.open("if (threadIdx.x == 0 && rb < row_end)")
+        w("double tot = 0.0;")
+        w("#pragma unroll")
+        w("for (int v = 0; v < %d; ++v) tot += s_wsum[v];" % WAVES)
+        store("tot", "rb")
+        w.close()
+        w.close()
+
+    w("// 2-4 twice: the common case (indptr[0] = 0, indptr[M] = nnz), where every range's")
+    w("// staged positions end where its owned ones do, without the code for other cases")
+    w.open("if (pbase == 0 && pend == nnz)")
+    phases(False)
     w.close()
-    w.close()
-    w("// otherwise the range it begins in sums it whole (below)")
-    w.close()
-    w.open("if (wv == %d && rb < n_rows && rb_s < p1)" % (1 if WAVES > 1 else 0))
-    w("const tg_i64 ef = (rb_s - pal) / %d, el0 = (rb_e - 1 - pal) / %d;" % (CH, CH))
-    w("const tg_i64 el = el0 < NL - 1 ? el0 : NL - 1;  // ranges past the grid's last do not exist")
-    w.open("if (el < %d)" % MERGE_CAP)
-    w("const int st = (int)((rb_s > p0 ? rb_s : p0) - pa);")
-    w("double t = 0.0;")
-    w("#pragma unroll 4")
-    w("for (int q = st + l; q < qhi; q += 64) t += s_prod[q];")
-    w("t = tg_segsum<64>(t);")
-    w("double tot = t;")
-    w.open("if (tg_mp_commit(tg_part, e, ef, el, t, &tot) && l == 0 && rb < row_end)")
-    store("tot", "rb")
-    w.close()
-    w.close()
-    w("// otherwise, when it begins here, this workgroup sums it whole (below)")
-    w.close()
-    w("// 3. the owned rows [ra, rb), %d row pointers at a time" % RB)
-    w("const int lane = threadIdx.x %% %d;" % TPR)
-    w("const int slot = threadIdx.x / %d;" % TPR)
-    w("#pragma unroll 1")
-    w.open("for (tg_i64 b0 = ra; b0 < rb; b0 += %d)" % RB)
-    w("const int nb = (int)(rb - b0 < %d ? rb - b0 : %d);" % (RB, RB))
-    w("for (int i = threadIdx.x; i <= nb; i += %d) s_ptr[i] = indptr[b0 + i];" % B)
-    w("__syncthreads();")
-    w("// rows of up to 64 nonzeros: one lane group each")
-    w("#pragma unroll 1")
-    w.open("for (int i = slot; i < nb; i += %d)" % SLOTS)
-    w("const tg_i64 rs = s_ptr[i], re = s_ptr[i + 1];")
-    w("const int st = (int)((rs > p0 ? rs : p0) - pa), en = (int)(re - pa);")
-    w("const bool mine = !(b0 + i == ra && ra_cut);  // a cut ra was committed above")
-    w("const bool own = mine && en - st <= 64 && en <= qhi;  // staged whole")
-    w("double acc = 0.0;")
-    w.open("if (own)")
-    w("#pragma unroll 4")
-    w("for (int q = st + lane; q < en; q += %d) acc += s_prod[q];" % TPR)
-    w.close()
-    w("if (mine && !own && lane == 0) s_long[atomicAdd(&s_nlong, 1)] = i;")
-    w("acc = tg_segsum<%d>(acc);" % TPR)
-    w.open("if (own && lane == 0 && b0 + i < row_end)")
-    store("acc", "b0 + i")
-    w.close()
-    w.close()
-    w("__syncthreads();")
-    w("// longer rows: one wave each")
-    w("const int nl = s_nlong;")
-    w("#pragma unroll 1")
-    w.open("for (int k = wv; k < nl; k += %d)" % WAVES)
-    w("const int i = s_long[k];")
-    w("const tg_i64 rs = s_ptr[i], re = s_ptr[i + 1];")
-    w("const int st = (int)((rs > p0 ? rs : p0) - pa), en = (int)(re - pa);")
-    w("double acc = 0.0;")
-    w("#pragma unroll 4")
-    w("for (int q = st + l; q < (en < qhi ? en : qhi); q += 64) acc += s_prod[q];")
-    tail("ps > rs ? ps : rs", "re", "acc")
-    w("acc = tg_segsum<64>(acc);")
-    w.open("if (l == 0 && b0 + i < row_end)")
-    store("acc", "b0 + i")
-    w.close()
-    w.close()
-    w("__syncthreads();  // every wave has read s_nlong, s_long and s_ptr")
-    w("if (threadIdx.x == 0) s_nlong = 0;")
-    w.close()
-    w("// 4. row rb, when it begins in this range and reaches past the scratch's last range:")
-    w("// summed whole by the whole workgroup with its own loads, the waves' sums added in")
-    w("// wave order (the condition is the same for every wave)")
-    w.open("if (rb < n_rows && rb_s < p1 && (rb_s - pal) / %d == e && "
-           "((rb_e - 1 - pal) / %d < NL - 1 ? (rb_e - 1 - pal) / %d : NL - 1) >= %d)"
-           % (CH, CH, CH, MERGE_CAP))
-    w("double t = 0.0;")
-    w("#pragma unroll 4")
-    w.open("for (tg_i64 pq = rb_s + (tg_i64)threadIdx.x; pq < rb_e; pq += %d)" % B)
-    w("const tg_i64 cq = indices[pq];")
-    w("t += %s;" % _value_with(plan, "data[pq]", gather("cq"), row, "cq"))
-    w.close()
-    w("t = tg_segsum<64>(t);")
-    w("if (l == 0) s_wsum[wv] = t;")
-    w("__syncthreads();")
-    w.open("if (threadIdx.x == 0 && rb < row_end)")
-    w("double tot = 0.0;")
-    w("#pragma unroll")
-    w("for (int v = 0; v < %d; ++v) tot += s_wsum[v];" % WAVES)
-    store("tot", "rb")
-    w.close()
+    w.open("else")
+    phases(True)
     w.close()
 
 
