@@ -15,14 +15,16 @@ from .codegen import Config
 TUNED: Dict[str, Config] = {
     # winners of an exhaustive sweep of the legal CDNA4 space on one MI355X,
     # cold (rotated) inputs, GPU-event kernel time
-    # 16 nonzeros per row, uniform random columns: tiles of 256 rows on 4-lane
+    # 16 nonzeros per row, uniform random columns: tiles of 224 rows on 4-lane
     # groups x 4 nonzeros (two row passes per group: every nonzero of the tile
-    # is one first-step item), the tile's 4096 gathers sorted by column in LDS
+    # is one first-step item), the tile's 3584 gathers sorted by column in LDS
     # so that each gather instruction's 64 lanes share cache lines of x;
-    # 12.3-12.4 us against 12.6 for the best direct-gather tiles
-    # (T16/TPR8/U2/B128) and 15.8 for the same tiles with direct gathers
-    # (interleaved repeats on one box)
-    "c1": Config(tile_size=256, threads_per_row=4, unroll=4, vector_width=1, block_size=512,
+    # 11.7 us against 11.8 for tiles of 256 rows (391 workgroups for 256 CUs,
+    # where 224 rows make 447 and leave fewer CUs with one), 12.6 for the best
+    # direct-gather tiles (T16/TPR8/U2/B128) and 15.8 for T256/TPR4/U4/B512
+    # with direct gathers (interleaved repeats on one box); below about 196
+    # rows the grid passes the 512 workgroups that fit at two per CU
+    "c1": Config(tile_size=224, threads_per_row=4, unroll=4, vector_width=1, block_size=512,
                  gather="sorted"),
     # 7 nonzeros per row: 4 lanes x 2
     "c2": Config(tile_size=128, threads_per_row=4, unroll=2, vector_width=1, block_size=256),
