@@ -24,9 +24,9 @@
  *     launch and changes nothing else: every nnz gives the product, bit for bit
  *     the same whenever nnz >= indptr[M] - indptr[0] (an undercount may sum
  *     some rows in another order).  No position outside [indptr[0], indptr[M])
- *     is used; the merge-path, hybrid and stream SpMV variants may load
- *     positions below nnz outside it (they start on nnz's numbers and check
- *     them against indptr);
+ *     is used; the merge-path, hybrid and stream SpMV variants and the row
+ *     tiles with sorted gathers may load positions below nnz outside it (they
+ *     start on nnz's numbers and check them against indptr);
  *   - indptr/indices are never written;
  *   - the call is synchronous (returns after the kernel finished);
  *   - it returns void: a failure is recorded and reported by tg_last_status()
