@@ -88,9 +88,33 @@ def test_placement_records_decode():
         (6 << 32) | (hw & ~0xFF))[1]                           # the wave's slot does not count
 
 
+def test_stream_probe_stays_in_its_padded_buffer():
+    """Workgroup w reads pairs w BLK U + k BLK + t: for any grid the last pair read
+    is the buffer's last, and the per-wave output has one slot per wave."""
+    blk, u = probes.STREAM_BLOCK, probes.STREAM_UNROLL
+    for grid in (1, 2, 7, 16384):
+        n2 = grid * blk * u
+        reads = {(w * blk * u + k * blk + t) for w in (0, grid - 1) for k in (0, u - 1)
+                 for t in (0, blk - 1)}
+        assert max(reads) == n2 - 1 and min(reads) == 0
+        assert ((grid - 1) * blk + blk - 1) >> 6 == grid * blk // 64 - 1
+    src = probes.stream_source("s")
+    assert src.count("__builtin_nontemporal_load(") == u and "if (" not in src.split("v[0] =")[1].split("double s")[0]
+
+
+def test_rowgather_probe_reads_inside_its_table():
+    src = probes.rowgather_source("r")
+    assert "if (row >= M) return;" in src
+    assert "cols + row * %d" % probes.ROWGATHER_ROW_NNZ in src
+    assert "(B + cc[k] * 64) + j" in src          # j < 32: 16 bytes of a 512-byte row
+
+
 def test_probes_compile_for_gfx950():
     name = "probe_placement_b1024_l45264"
     code = probes._code_object(name, probes.placement_source(name, 1024, 45264, 2000))
     assert code[:4] == b"\x7fELF"
+    for nm, text in (("probe_stream_cpu", probes.stream_source("probe_stream_cpu")),
+                     ("probe_rowgather_cpu", probes.rowgather_source("probe_rowgather_cpu"))):
+        assert probes._code_object(nm, text)[:4] == b"\x7fELF"
     n = probes.build(orders=("matrix", "lsort"), shapes=((512, 8),), gathers=("x",))
     assert n == 2

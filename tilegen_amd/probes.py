@@ -41,6 +41,14 @@ several grid sizes and reports how many CUs took them and how many took two or
 more (``run_placement``):
 
     python -m tilegen_amd.probes placement --grids 194,239,256 --block 1024 --lds 45264
+
+``stream`` reads a buffer once with 128-bit loads, cold over rotated copies at each
+size and re-reading one resident buffer (``run_stream``); ``rowgather`` makes SpMM's
+512-byte row gathers from a 64-wide fp64 table, 16 per output row, with no values or
+FMAs (``run_rowgather``):
+
+    python -m tilegen_amd.probes stream --mib 8,27,128,512 --resident-mib 96
+    python -m tilegen_amd.probes rowgather --table-rows 100000,6250
 """
 
 from __future__ import annotations
@@ -296,6 +304,134 @@ def _function(name: str, src: str) -> int:
     return int(fn.value)
 
 
+STREAM_BLOCK, STREAM_UNROLL = 256, 8
+
+
+def stream_source(name: str) -> str:
+    """``stream``: a plain read of n2 16-byte pairs.  Workgroup w reads the
+    contiguous pairs [w BLK U, (w+1) BLK U), lane t the pairs k BLK + t, every load
+    issued before any is used (the buffer is padded to whole workgroups, so no load
+    is conditional); one double per wave is written so that the loads stay live."""
+    blk, u = STREAM_BLOCK, STREAM_UNROLL
+    L = ["typedef double tg_f64x2 __attribute__((ext_vector_type(2)));",
+         'extern "C" __global__ __launch_bounds__(%d)' % blk,
+         "void %s(const double* __restrict__ a, double* __restrict__ out) {" % name,
+         "  const long long t = (long long)blockIdx.x * %d + threadIdx.x;" % blk,
+         "  const tg_f64x2* p = (const tg_f64x2*)a + (long long)blockIdx.x * %d + threadIdx.x;"
+         % (blk * u),
+         "  tg_f64x2 v[%d];" % u]
+    L += ["  v[%d] = __builtin_nontemporal_load(p + %d);" % (k, k * blk) for k in range(u)]
+    L += ["  double s = 0.0;"]
+    L += ["  s += v[%d].x + v[%d].y;" % (k, k) for k in range(u)]
+    L += ["  for (int d = 32; d >= 1; d >>= 1) s += __shfl_xor(s, d);",
+          "  if ((threadIdx.x & 63) == 0) out[t >> 6] = s;",
+          "}", ""]
+    return "\n".join(L)
+
+
+def run_stream(sizes_mib: Sequence[float], resident_mib: Sequence[float], warmup: int,
+               iters: int) -> List[dict]:
+    """Read rate of the ``stream`` probe: over rotated copies (cold, so every launch
+    reads HBM) at each size, and re-reading one buffer (resident in the Infinity
+    Cache when it fits its 256 MB)."""
+    from . import runtime as rt
+    from .profiling import bench_copies
+    name = "probe_stream_b%du%d" % (STREAM_BLOCK, STREAM_UNROLL)
+    fn = _function(name, stream_source(name))
+    per_launch = STREAM_BLOCK * STREAM_UNROLL      # pairs per workgroup
+    out = []
+    for mode, sizes in (("cold", sizes_mib), ("resident", resident_mib)):
+        for mib in sizes:
+            grid = max(1, int(round(mib * (1 << 20) / (16 * per_launch))))
+            n2 = grid * per_launch
+            copies = bench_copies(16 * n2) if mode == "cold" else 1
+            rng = np.random.default_rng(7)
+            host = rng.uniform(-1, 1, 2 * n2)
+            bufs = [rt.DeviceBuffer(host) for _ in range(copies)]
+            outs = [rt.DeviceBuffer(nbytes=grid * STREAM_BLOCK // 64 * 8) for _ in range(copies)]
+            sets = [[b, o] for b, o in zip(bufs, outs)]
+            rt.launch(fn, grid, STREAM_BLOCK, 0, sets[0])
+            got = float(outs[0].to_host(np.empty(grid * STREAM_BLOCK // 64)).sum())
+            want = float(host.sum())
+            assert abs(got - want) <= 1e-9 * max(1.0, float(np.abs(host).sum())), (got, want)
+            kms, _ = rt.time_launches(fn, grid, STREAM_BLOCK, 0, sets, warmup, iters)
+            us = float(np.mean(kms)) * 1e3
+            out.append({"probe": "stream", "mode": mode, "mib": round(16 * n2 / (1 << 20), 2),
+                        "copies": copies, "us_avg": round(us, 3),
+                        "us_median": round(float(np.median(kms)) * 1e3, 3),
+                        "tb_s": round(16 * n2 / (us * 1e-6) / 1e12, 3)})
+            for b in bufs + outs:
+                b.free()
+    return out
+
+
+ROWGATHER_ROW_NNZ = 16
+
+
+def rowgather_source(name: str) -> str:
+    """``rowgather``: SpMM's row gathers without values or FMAs.  A 32-lane group
+    takes one output row of ROWGATHER_ROW_NNZ column indices; lane j loads 16 bytes
+    of each gathered 512-byte row of the 64-wide table, four rows in flight, adds
+    them and writes its 16 bytes of the output row."""
+    L = ["typedef double tg_f64x2 __attribute__((ext_vector_type(2)));",
+         'extern "C" __global__ __launch_bounds__(256)',
+         "void %s(const long long* __restrict__ cols, const double* __restrict__ B," % name,
+         "        double* __restrict__ C, const long long M) {",
+         "  const long long row = (long long)blockIdx.x * 8 + (threadIdx.x >> 5);",
+         "  const int j = threadIdx.x & 31;",
+         "  if (row >= M) return;",
+         "  const long long* c = cols + row * %d;" % ROWGATHER_ROW_NNZ,
+         "  tg_f64x2 acc = {0.0, 0.0};",
+         "  #pragma unroll",
+         "  for (int q = 0; q < %d; q += 4) {" % ROWGATHER_ROW_NNZ,
+         "    long long cc[4];",
+         "    #pragma unroll",
+         "    for (int k = 0; k < 4; ++k) cc[k] = c[q + k];",
+         "    tg_f64x2 v[4];",
+         "    #pragma unroll",
+         "    for (int k = 0; k < 4; ++k) v[k] = *((const tg_f64x2*)(B + cc[k] * 64) + j);",
+         "    #pragma unroll",
+         "    for (int k = 0; k < 4; ++k) acc += v[k];",
+         "  }",
+         "  __builtin_nontemporal_store(acc, (tg_f64x2*)(C + row * 64) + j);",
+         "}", ""]
+    return "\n".join(L)
+
+
+def run_rowgather(table_rows: Sequence[int], M: int, warmup: int, iters: int,
+                  seed: int = 11) -> List[dict]:
+    """Gathered rate of the ``rowgather`` probe: M x 16 random rows of a
+    table_rows x 64 fp64 table, cold (rotated copies of table, indices and output)."""
+    from . import runtime as rt
+    from .profiling import bench_copies
+    name = "probe_rowgather"
+    fn = _function(name, rowgather_source(name))
+    out = []
+    for n in table_rows:
+        rng = np.random.default_rng(seed)
+        cols = rng.integers(0, n, M * ROWGATHER_ROW_NNZ).astype(np.int64)
+        table = rng.uniform(-1, 1, (n, 64))
+        nbytes = 8 * cols.size + 8 * table.size + 8 * M * 64
+        copies = bench_copies(nbytes)
+        sets = [[rt.DeviceBuffer(cols), rt.DeviceBuffer(table), rt.DeviceBuffer(nbytes=M * 64 * 8), M]
+                for _ in range(copies)]
+        grid = -(-M // 8)
+        rt.launch(fn, grid, 256, 0, sets[0])
+        got = sets[0][2].to_host(np.empty((M, 64)))
+        want = table[cols].reshape(M, ROWGATHER_ROW_NNZ, 64).sum(axis=1)
+        assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+        kms, _ = rt.time_launches(fn, grid, 256, 0, sets, warmup, iters)
+        us = float(np.mean(kms)) * 1e3
+        out.append({"probe": "rowgather", "table_mb": round(8 * table.size / 1e6, 1),
+                    "gathers": int(cols.size), "copies": copies, "us_avg": round(us, 3),
+                    "us_median": round(float(np.median(kms)) * 1e3, 3),
+                    "gathered_tb_s": round(cols.size * 512 / (us * 1e-6) / 1e12, 3)})
+        for st in sets:
+            for b in st[:3]:
+                b.free()
+    return out
+
+
 def placement_source(name: str, blk: int, lds_bytes: int, spin_ticks: int) -> str:
     """``placement``: where the dispatcher puts the workgroups of a grid.  Each
     workgroup of ``blk`` lanes and ``lds_bytes`` of static LDS (the footprint of the
@@ -492,7 +628,12 @@ def run_flat(case_id: str, orders: Sequence[str], shapes: Sequence[Tuple[int, in
 
 def main(argv: Optional[Sequence[str]] = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("probe", nargs="?", choices=["flat", "placement"], default="flat")
+    ap.add_argument("probe", nargs="?", choices=["flat", "placement", "stream", "rowgather"],
+                    default="flat")
+    ap.add_argument("--mib", default="8,27,128,512", help="stream: cold read sizes (MiB)")
+    ap.add_argument("--resident-mib", default="96", help="stream: re-read sizes (MiB)")
+    ap.add_argument("--table-rows", default="100000,6250", help="rowgather: table rows")
+    ap.add_argument("--rows", type=int, default=100000, help="rowgather: output rows")
     ap.add_argument("--grids", default="194,207,222,239,250,256,259",
                     help="placement: grid sizes")
     ap.add_argument("--block", type=int, default=1024, help="placement: workgroup size")
@@ -525,11 +666,22 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
             nm = "probe_placement_b%d_l%d" % (blk, lds)
             _code_object(nm, placement_source(nm, blk, lds, 2000))
             n += 1
+        nm = "probe_stream_b%du%d" % (STREAM_BLOCK, STREAM_UNROLL)
+        _code_object(nm, stream_source(nm))
+        _code_object("probe_rowgather", rowgather_source("probe_rowgather"))
+        n += 2
         print("built %d probe code objects in %.1fs" % (n, time.time() - t0))
         return 0
     if args.probe == "placement":
         grids = [int(g) for g in args.grids.split(",") if g]
         recs = run_placement(grids, args.block, args.lds)
+    elif args.probe == "stream":
+        recs = run_stream([float(m) for m in args.mib.split(",") if m],
+                          [float(m) for m in args.resident_mib.split(",") if m],
+                          args.warmup, args.iters)
+    elif args.probe == "rowgather":
+        recs = run_rowgather([int(n) for n in args.table_rows.split(",") if n], args.rows,
+                             args.warmup, args.iters)
     else:
         recs = run_flat(args.case, orders, shapes, gathers, args.seg, args.warmup, args.iters,
                         args.repeats, not args.no_control)

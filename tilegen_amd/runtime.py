@@ -233,7 +233,12 @@ class DeviceBuffer:
 
     def to_host(self, out: Optional[np.ndarray] = None) -> np.ndarray:
         if out is None:
+            if self.array is None:
+                raise ValueError("DeviceBuffer made from a byte count has no host shape: "
+                                 "pass out=")
             out = np.empty_like(self.array)
+        if not out.flags.c_contiguous or out.nbytes < self.nbytes:
+            raise ValueError("to_host: out must be C-contiguous and hold %d bytes" % self.nbytes)
         if self.nbytes:
             check(lib().tg_memcpy_dtoh(out.ctypes.data, self.ptr, self.nbytes), "tg_memcpy_dtoh")
         return out
