@@ -109,6 +109,18 @@ def test_rowgather_probe_reads_inside_its_table():
     assert "(B + cc[k] * 64) + j" in src          # j < 32: 16 bytes of a 512-byte row
 
 
+def test_gather_model_follows_the_kernel_hash():
+    """The gather probe's numpy model replays the kernel's xorshift: every index is
+    below n, inactive lanes add nothing, and one wave's sum is its lanes' sums."""
+    x = np.arange(1000, dtype=np.float64)
+    full = probes.gather_expected(1, 64, x)
+    half = probes.gather_expected(1, 32, x)
+    assert full.shape == (probes.GATHER_BLOCK // 64,)
+    assert np.all(half <= full) and np.all(half > 0)
+    src = probes.gather_source("g", 32)
+    assert "(threadIdx.x & 63) < 32" in src and "x[h % n]" in src
+
+
 def test_probes_compile_for_gfx950():
     name = "probe_placement_b1024_l45264"
     code = probes._code_object(name, probes.placement_source(name, 1024, 45264, 2000))

@@ -49,6 +49,12 @@ FMAs (``run_rowgather``):
 
     python -m tilegen_amd.probes stream --mib 8,27,128,512 --resident-mib 96
     python -m tilegen_amd.probes rowgather --table-rows 100000,6250
+
+``gather`` makes random 8-byte loads from an L2-resident array of 100000 doubles at
+addresses hashed in registers, with 64, 32 or 16 lanes of each wave active
+(``run_gather``):
+
+    python -m tilegen_amd.probes gather --active 64,32,16
 """
 
 from __future__ import annotations
@@ -365,6 +371,81 @@ def run_stream(sizes_mib: Sequence[float], resident_mib: Sequence[float], warmup
     return out
 
 
+GATHER_BLOCK, GATHER_PER_LANE = 256, 64
+
+
+def gather_source(name: str, active: int) -> str:
+    """``gather``: random 8-byte loads from an array of n doubles (L2-resident at
+    0.8 MB).  The first ``active`` lanes of each wave make GATHER_PER_LANE loads at
+    indices hashed in registers (no index stream), 8 in flight; one double per wave
+    is written so that the loads stay live."""
+    return "\n".join([
+        'extern "C" __global__ __launch_bounds__(%d)' % GATHER_BLOCK,
+        "void %s(const double* __restrict__ x, double* __restrict__ out, const unsigned n) {"
+        % name,
+        "  const unsigned t = blockIdx.x * %du + threadIdx.x;" % GATHER_BLOCK,
+        "  double s = 0.0;",
+        "  if ((threadIdx.x & 63) < %d) {" % active,
+        "    unsigned h = t * 0x9E3779B9u + 0x7F4A7C15u;",
+        "    #pragma unroll 1",
+        "    for (int k = 0; k < %d; k += 8) {" % GATHER_PER_LANE,
+        "      double v[8];",
+        "      #pragma unroll",
+        "      for (int j = 0; j < 8; ++j) {",
+        "        h ^= h << 13; h ^= h >> 17; h ^= h << 5;   // xorshift32",
+        "        v[j] = x[h % n];",
+        "      }",
+        "      #pragma unroll",
+        "      for (int j = 0; j < 8; ++j) s += v[j];",
+        "    }",
+        "  }",
+        "  for (int d = 32; d >= 1; d >>= 1) s += __shfl_xor(s, d);",
+        "  if ((threadIdx.x & 63) == 0) out[t >> 6] = s;",
+        "}", ""])
+
+
+def gather_expected(grid: int, active: int, x: np.ndarray) -> np.ndarray:
+    """What the gather probe writes: per wave, the sum of its active lanes' loads."""
+    n = np.uint32(len(x))
+    lanes = np.arange(grid * GATHER_BLOCK, dtype=np.uint64)
+    act = (lanes & 63) < active
+    h = ((lanes * 0x9E3779B9 + 0x7F4A7C15) & 0xFFFFFFFF).astype(np.uint32)
+    s = np.zeros(lanes.size)
+    for _ in range(GATHER_PER_LANE):
+        h ^= h << np.uint32(13)
+        h ^= h >> np.uint32(17)
+        h ^= h << np.uint32(5)
+        s += np.where(act, x[h % n], 0.0)
+    return s.reshape(-1, 64).sum(axis=1)
+
+
+def run_gather(actives: Sequence[int], n: int, waves: int, warmup: int, iters: int
+               ) -> List[dict]:
+    """Random-gather rate (G gathered addresses per second) from an n-double array."""
+    from . import runtime as rt
+    x = np.random.default_rng(5).uniform(-1, 1, n)
+    bx = rt.DeviceBuffer(x)
+    grid = max(1, waves * 64 // GATHER_BLOCK)
+    bout = rt.DeviceBuffer(nbytes=grid * GATHER_BLOCK // 64 * 8)
+    out = []
+    for a in actives:
+        name = "probe_gather_a%d" % a
+        fn = _function(name, gather_source(name, a))
+        args = [bx, bout, np.uint32(n)]
+        rt.launch(fn, grid, GATHER_BLOCK, 0, args)
+        got = bout.to_host(np.empty(grid * GATHER_BLOCK // 64))
+        assert np.allclose(got, gather_expected(grid, a, x), rtol=1e-10, atol=1e-10)
+        kms, _ = rt.time_launches(fn, grid, GATHER_BLOCK, 0, [args], warmup, iters)
+        us = float(np.mean(kms)) * 1e3
+        g = grid * GATHER_BLOCK // 64 * a * GATHER_PER_LANE
+        out.append({"probe": "gather", "active_lanes": a, "array_kb": n * 8 // 1024,
+                    "gathers": g, "us_avg": round(us, 3),
+                    "g_gathers_per_s": round(g / (us * 1e-6) / 1e9, 1)})
+    bx.free()
+    bout.free()
+    return out
+
+
 ROWGATHER_ROW_NNZ = 16
 
 
@@ -628,8 +709,10 @@ def run_flat(case_id: str, orders: Sequence[str], shapes: Sequence[Tuple[int, in
 
 def main(argv: Optional[Sequence[str]] = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("probe", nargs="?", choices=["flat", "placement", "stream", "rowgather"],
-                    default="flat")
+    ap.add_argument("probe", nargs="?",
+                    choices=["flat", "placement", "stream", "rowgather", "gather"], default="flat")
+    ap.add_argument("--active", default="64,32,16", help="gather: active lanes per wave")
+    ap.add_argument("--waves", type=int, default=65536, help="gather: waves launched")
     ap.add_argument("--mib", default="8,27,128,512", help="stream: cold read sizes (MiB)")
     ap.add_argument("--resident-mib", default="96", help="stream: re-read sizes (MiB)")
     ap.add_argument("--table-rows", default="100000,6250", help="rowgather: table rows")
@@ -670,6 +753,9 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
         _code_object(nm, stream_source(nm))
         _code_object("probe_rowgather", rowgather_source("probe_rowgather"))
         n += 2
+        for act in (64, 32, 16):
+            _code_object("probe_gather_a%d" % act, gather_source("probe_gather_a%d" % act, act))
+            n += 1
         print("built %d probe code objects in %.1fs" % (n, time.time() - t0))
         return 0
     if args.probe == "placement":
@@ -678,6 +764,9 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
     elif args.probe == "stream":
         recs = run_stream([float(m) for m in args.mib.split(",") if m],
                           [float(m) for m in args.resident_mib.split(",") if m],
+                          args.warmup, args.iters)
+    elif args.probe == "gather":
+        recs = run_gather([int(a) for a in args.active.split(",") if a], 100000, args.waves,
                           args.warmup, args.iters)
     elif args.probe == "rowgather":
         recs = run_rowgather([int(n) for n in args.table_rows.split(",") if n], args.rows,
