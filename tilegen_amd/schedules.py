@@ -31,13 +31,14 @@ TUNED: Dict[str, Config] = {
     # skewed rows, stream ranges: every workgroup takes an equal range of B x U
     # nonzeros and sums, from LDS, the rows that end in it.
     # c3a (power-law rows, half of them one nonzero long): ranges of 4096 (1024
-    # lanes x 4), rows summed by 4-lane groups; 11.3-11.8 us against 12.2 for ranges
-    # of 2048, 13.6-14.1 for the best hybrid tiles (T64/TPR4/U4/B256) and 17.4 for
-    # row tiles alone (interleaved bench repeats on one box).
+    # lanes x 4), rows summed by 2-lane groups; 11.4 us against 11.7 with 4-lane
+    # groups, 11.6 with one lane per row and 12.1 for ranges of 2048, 13.6-14.1 for the
+    # best hybrid tiles (T64/TPR4/U4/B256) and 17.4 for row tiles alone (interleaved
+    # repeats on one box).
     # c3b (1% of rows 2000 long, the rest 4): ranges of 2048 (512 lanes x 4), one
     # lane per short row; 6.9-7.1 us against 7.4-7.7 for the best hybrid tiles
     # (T128/TPR4/U2/B512) and 10.6 for the best row tiles (T32/TPR32/U2/B1024)
-    "c3a": Config(tile_size=256, threads_per_row=4, unroll=4, vector_width=1, block_size=1024,
+    "c3a": Config(tile_size=512, threads_per_row=2, unroll=4, vector_width=1, block_size=1024,
                   balance="stream"),
     "c3b": Config(tile_size=512, threads_per_row=1, unroll=4, vector_width=1, block_size=512,
                   balance="stream"),
