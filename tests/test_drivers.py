@@ -36,17 +36,20 @@ def test_verify_all_cpu(tmp_path):
 
 @pytest.mark.gpu
 def test_verify_all_hip_balance_forms(tmp_path, hip_ready):
-    """On the HIP backend spmv also runs in its merge-path, hybrid and stream forms."""
+    """On the HIP backend spmv also runs in its merge-path, hybrid and stream forms
+    and as row tiles with sorted gathers."""
     _write_tiny(str(tmp_path))
     payload = verify_all.run(str(tmp_path), "hip", classes=["tiny"], kernels=["spmv"],
                              workdir=str(tmp_path / "gen"), log=lambda m: None)
     s = payload["summary"]
     assert s["executed"] and s["balance_triples"] == len(verify_all.BALANCE_CONFIGS)
-    assert s["normal_triples"] == len(verify_all.CONFIGS) + len(verify_all.BALANCE_CONFIGS)
+    assert s["sorted_triples"] == s["sorted_passed"] == len(verify_all.SORTED_CONFIGS)
+    assert s["normal_triples"] == (len(verify_all.CONFIGS) + len(verify_all.BALANCE_CONFIGS) +
+                                   len(verify_all.SORTED_CONFIGS))
     assert s["all_normal_passed"] and s["all_bugs_caught"]
     md = verify_all.render_table(payload)
     assert md.count("/hybrid |") == 2 and md.count("/nnz |") == 2
-    assert md.count("/stream |") == 2
+    assert md.count("/stream |") == 2 and md.count("/sorted |") == 2
 
 
 def test_tune_all_cpu(tmp_path):

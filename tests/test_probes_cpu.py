@@ -128,5 +128,6 @@ def test_probes_compile_for_gfx950():
     for nm, text in (("probe_stream_cpu", probes.stream_source("probe_stream_cpu")),
                      ("probe_rowgather_cpu", probes.rowgather_source("probe_rowgather_cpu"))):
         assert probes._code_object(nm, text)[:4] == b"\x7fELF"
-    n = probes.build(orders=("matrix", "lsort"), shapes=((512, 8),), gathers=("x",))
+    n = probes.build(orders=("matrix", "lsort"), shapes=((512, 8),), gathers=("x",),
+                     others=False)
     assert n == 2

@@ -2106,6 +2106,8 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w("double acc[%d];" % R)
     if coop:
         w("bool coop[%d];" % R)
+    else:
+        w("bool lv[%d];  // the lane's row exists" % R)
     w("#pragma unroll")
     w.open("for (int r = 0; r < %d; ++r)" % R)
     w("const int lr = slot + r * %d;" % SLOTS)
@@ -2118,6 +2120,7 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("const tg_i64 ri = live ? row0 + lr : 0;")
         w("rs[r] = live ? indptr[ri] : 0;")
         w("re[r] = live ? indptr[ri + 1] : 0;")
+        w("lv[r] = live;")
     if coop:
         skip = ""
         if hybrid:
@@ -2145,6 +2148,18 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w.close()
     w("acc[r] = 0.0;")
     w.close()
+    if not low.tiled:
+        w("// the positions of the wave's rows of each pass, [wlo, whi): the rows ascend with")
+        w("// the lane, so these are the first live row's start and the last one's end; a load")
+        w("// anywhere in them stays inside the launch's positions")
+        w("tg_i64 wlo[%d], whi[%d];" % (R, R))
+        w("#pragma unroll")
+        w.open("for (int r = 0; r < %d; ++r)" % R)
+        w("const unsigned long long m = __ballot(lv[r]);")
+        w("const int f = m ? (int)__builtin_ctzll(m) : 0, g = m ? 63 - (int)__builtin_clzll(m) : 0;")
+        w("wlo[r] = m ? __shfl(rs[r], f) : 0;")
+        w("whi[r] = m ? __shfl(re[r], g) : 0;")
+        w.close()
 
     # every row's first step held at once costs about 6 R U registers per lane: past
     # R U = 8 that spills, so such schedules keep one guarded step per row
@@ -2156,7 +2171,7 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
         w("(void)row;")
         w("const tg_i64 q = (rs[r] & ~(tg_i64)%d) + (tg_i64)lane * %d;" % (ALIGN - 1, U))
         w.open("if (q < re[r] && rs[r] < re[r])")
-        step("q", "rs[r]", "re[r]", "acc[r]", *(() if low.tiled else ("rs[r]", "re[r]")))
+        step("q", "rs[r]", "re[r]", "acc[r]", *(() if low.tiled else ("wlo[r]", "whi[r]")))
         w.close()
         w.close()
     else:
@@ -2223,7 +2238,7 @@ def _hip_scalar_reduce(w: _W, plan: Plan, low: Lowering, bound: str, geo: Launch
     w("#pragma unroll 1")
     w.open("for (tg_i64 q = (rs[r] & ~(tg_i64)%d) + (tg_i64)lane * %d + %d; q < re[r]; q += %d)"
            % (ALIGN - 1, U, STEP, STEP))
-    step("q", "rs[r]", "re[r]", "acc[r]", *(() if low.tiled else ("rs[r]", "re[r]")))
+    step("q", "rs[r]", "re[r]", "acc[r]", *(() if low.tiled else ("wlo[r]", "whi[r]")))
     w.close()
     w.close()
     w("#pragma unroll")

@@ -617,11 +617,23 @@ def lsort_shift(N: int, nb: int) -> int:
 
 
 def build(orders=("matrix", "b9", "line", "lsort"), shapes=((1024, 4), (1024, 8), (512, 8)),
-          gathers=("x", "none", "one"), seg: int = 4) -> int:
+          gathers=("x", "none", "one"), seg: int = 4, others: bool = True) -> int:
+    """Compile the flat probe's variants and (``others``) the placement, stream,
+    rowgather and gather probes into the kernel cache; returns how many."""
     n = 0
     for name, o, blk, u, g in _variants(orders, shapes, gathers, seg):
         _code_object(name, _source(name, o, blk, u, seg, g))
         n += 1
+    if others:
+        for blk, lds in ((1024, 45264), (512, 28816)):
+            nm = "probe_placement_b%d_l%d" % (blk, lds)
+            _code_object(nm, placement_source(nm, blk, lds, 2000))
+        nm = "probe_stream_b%du%d" % (STREAM_BLOCK, STREAM_UNROLL)
+        _code_object(nm, stream_source(nm))
+        _code_object("probe_rowgather", rowgather_source("probe_rowgather"))
+        for act in (64, 32, 16):
+            _code_object("probe_gather_a%d" % act, gather_source("probe_gather_a%d" % act, act))
+        n += 7
     return n
 
 
@@ -745,17 +757,6 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
     if args.build:
         t0 = time.time()
         n = build(orders, shapes, gathers, args.seg)
-        for blk, lds in ((1024, 45264), (512, 28816)):
-            nm = "probe_placement_b%d_l%d" % (blk, lds)
-            _code_object(nm, placement_source(nm, blk, lds, 2000))
-            n += 1
-        nm = "probe_stream_b%du%d" % (STREAM_BLOCK, STREAM_UNROLL)
-        _code_object(nm, stream_source(nm))
-        _code_object("probe_rowgather", rowgather_source("probe_rowgather"))
-        n += 2
-        for act in (64, 32, 16):
-            _code_object("probe_gather_a%d" % act, gather_source("probe_gather_a%d" % act, act))
-            n += 1
         print("built %d probe code objects in %.1fs" % (n, time.time() - t0))
         return 0
     if args.probe == "placement":

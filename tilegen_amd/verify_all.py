@@ -7,8 +7,8 @@ list, ``verify_all.py:27-31``) x the six corpus classes, plus one variant with
 SciPy.  On the HIP backend the SpMV-shaped kernels (spmv, fused_spmv_axpy)
 also run in the three load-balanced forms this build adds (``Config.balance``
 "nnz" for merge-path windows, "hybrid" for row tiles plus long-row workgroups
-and "stream" for equal nonzero ranges), counted apart from the reference's
-triples.  The result file has
+and "stream" for equal nonzero ranges) and as row tiles with sorted gathers
+(``Config.gather="sorted"``), counted apart from the reference's triples.  The result file has
 the reference's ``results/correctness.json``
 layout (``summary`` + per-triple ``results``), with the normwise errors and
 the indptr/indices byte check of this build added to each record.
@@ -32,7 +32,8 @@ from .env import probe
 from .matrices import build_corpus, corpus_classes
 from .verify import verify
 
-__all__ = ["KERNELS", "CONFIGS", "BALANCE_CONFIGS", "BUG_CONFIG", "run", "main"]
+__all__ = ["KERNELS", "CONFIGS", "BALANCE_CONFIGS", "SORTED_CONFIGS", "BUG_CONFIG", "run",
+           "main"]
 
 KERNELS = ["spmv", "spmm", "sddmm", "fused_spmv_axpy", "axpy"]
 CONFIGS = [
@@ -51,17 +52,25 @@ BALANCE_CONFIGS = [
     Config(tile_size=16, threads_per_row=8, unroll=2, vector_width=1, block_size=128,
            balance=b) for b in ("nnz", "hybrid", "stream")
 ]
+# HIP only: row tiles whose first-step gathers are sorted by column in LDS
+SORTED_CONFIGS = [
+    Config(tile_size=64, threads_per_row=4, unroll=4, vector_width=1, block_size=256,
+           gather="sorted"),
+    Config(tile_size=224, threads_per_row=4, unroll=4, vector_width=1, block_size=512,
+           gather="sorted"),
+]
 
 
 def run(matrix_dir: str, backend: str, classes: Optional[Sequence[str]] = None,
         kernels: Sequence[str] = KERNELS, configs: Sequence[Config] = CONFIGS,
         workdir: str = "build/generated", log=print,
         balance_configs: Optional[Sequence[Config]] = None) -> Dict[str, Any]:
-    """Every normal triple, the balance forms (HIP backend; ``balance_configs``
-    defaults to BALANCE_CONFIGS there and to none on the CPU backend, whose
-    emitter has row tiles only), and one injected bug per class."""
+    """Every normal triple, the forms this build adds (HIP backend;
+    ``balance_configs`` defaults to BALANCE_CONFIGS + SORTED_CONFIGS there and to
+    none on the CPU backend, whose emitter has row tiles with direct gathers only),
+    and one injected bug per class."""
     if balance_configs is None:
-        balance_configs = BALANCE_CONFIGS if backend == "hip" else []
+        balance_configs = BALANCE_CONFIGS + SORTED_CONFIGS if backend == "hip" else []
     classes = list(classes or corpus_classes())
     missing = [c for c in classes if not os.path.exists(os.path.join(matrix_dir, c + ".npz"))]
     if missing:
@@ -80,6 +89,7 @@ def run(matrix_dir: str, backend: str, classes: Optional[Sequence[str]] = None,
         results.append(verify("spmv", BUG_CONFIG, path, backend=backend, workdir=workdir))
     normal = [r for r in results if not r.inject_bug]
     balanced = [r for r in normal if (r.config or {}).get("balance", "rows") != "rows"]
+    sorted_ = [r for r in normal if (r.config or {}).get("gather", "direct") != "direct"]
     buggy = [r for r in results if r.inject_bug]
     executed = all(getattr(r, "executed", True) for r in results)
     summary = {
@@ -90,6 +100,8 @@ def run(matrix_dir: str, backend: str, classes: Optional[Sequence[str]] = None,
         "normal_passed": sum(1 for r in normal if r.ok),
         "balance_triples": len(balanced),
         "balance_passed": sum(1 for r in balanced if r.ok),
+        "sorted_triples": len(sorted_),
+        "sorted_passed": sum(1 for r in sorted_ if r.ok),
         "bug_triples": len(buggy),
         "bug_caught": sum(1 for r in buggy if not r.ok),
         "max_abs_err": max((r.max_abs_err for r in normal), default=0.0),
@@ -115,17 +127,20 @@ def render_table(payload: Dict[str, Any]) -> str:
                                           c.get("block_size"))
         if c.get("balance", "rows") != "rows":
             sched += "/" + c["balance"]
+        if c.get("gather", "direct") != "direct":
+            sched += "/" + c["gather"]
         lines.append("| %s | %s | %s | %s | %d | %d | %.3e | %.3e | %s |" % (
             r["matrix_class"], r["kernel"], sched, "PASS" if r["ok"] else "FAIL", r["rows"],
             r["nnz"], r["max_abs_err"], r.get("rel_err_inf", 0.0),
             "yes" if r["inject_bug"] else ""))
     head = [
         "# Differential test, %s backend" % s["backend"], "",
-        "normal triples passed: %d / %d (of which load-balanced forms: %d / %d); "
-        "injected bugs caught: %d / %d; max abs err %.3e; "
+        "normal triples passed: %d / %d (of which load-balanced forms: %d / %d, sorted-gather "
+        "tiles: %d / %d); injected bugs caught: %d / %d; max abs err %.3e; "
         "max normwise relative error %.3e (inf-norm), %.3e (2-norm); indptr/indices intact: %s."
         % (s["normal_passed"], s["normal_triples"], s.get("balance_passed", 0),
-           s.get("balance_triples", 0), s["bug_caught"], s["bug_triples"],
+           s.get("balance_triples", 0), s.get("sorted_passed", 0), s.get("sorted_triples", 0),
+           s["bug_caught"], s["bug_triples"],
            s["max_abs_err"], s["max_rel_err_inf"], s["max_rel_err_2"], s["structure_intact"]),
         "", "Written by `python -m tilegen_amd.verify_all`.", ""]
     return "\n".join(head + lines) + "\n"
