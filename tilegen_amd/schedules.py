@@ -15,16 +15,17 @@ from .codegen import Config
 TUNED: Dict[str, Config] = {
     # winners of an exhaustive sweep of the legal CDNA4 space on one MI355X,
     # cold (rotated) inputs, GPU-event kernel time
-    # 16 nonzeros per row, uniform random columns: tiles of 224 rows on 4-lane
-    # groups x 4 nonzeros (two row passes per group: every nonzero of the tile
-    # is one first-step item), the tile's 3584 gathers sorted by column in LDS
-    # so that each gather instruction's 64 lanes share cache lines of x;
-    # 11.7 us against 11.8 for tiles of 256 rows (391 workgroups for 256 CUs,
-    # where 224 rows make 447 and leave fewer CUs with one), 12.6 for the best
-    # direct-gather tiles (T16/TPR8/U2/B128) and 15.8 for T256/TPR4/U4/B512
-    # with direct gathers (interleaved repeats on one box); below about 196
-    # rows the grid passes the 512 workgroups that fit at two per CU
-    "c1": Config(tile_size=224, threads_per_row=4, unroll=4, vector_width=1, block_size=512,
+    # 16 nonzeros per row, uniform random columns: tiles of 240 rows, one per
+    # 4-lane group (15 waves, every nonzero of the tile one first-step item), the
+    # tile's 3840 gathers sorted by column in LDS so that each gather
+    # instruction's 64 lanes share cache lines of x.  11.4 us against 11.6 for
+    # 256 rows on 1024 lanes, 11.7 for 224 rows on 512 lanes (two rows per
+    # group), 12.6 for the best direct-gather tiles (T16/TPR8/U2/B128)
+    # (interleaved repeats on one box; a sweep of all 310 legal sorted schedules
+    # found the 1024-lane form first).  Two workgroups of 960 lanes share a CU
+    # (62 VGPRs, 67.5 KB of LDS each); two of 832 or 896 lanes did not, and took
+    # 15.6-15.8 us
+    "c1": Config(tile_size=240, threads_per_row=4, unroll=4, vector_width=1, block_size=960,
                  gather="sorted"),
     # 7 nonzeros per row: 4 lanes x 2
     "c2": Config(tile_size=128, threads_per_row=4, unroll=2, vector_width=1, block_size=256),
