@@ -118,10 +118,11 @@ def _structure_unchanged(bufs, ip, nnz):
         assert np.array_equal(got, np.arange(start, start + 4096, dtype=np.int64) % N)
 
 
-# row tiles, the tuned stream ranges (4096 and 2048 nonzeros), hybrid tiles and
-# merge-path windows; at this size every long row from about p = 2^28 on has
-# pieces past the 65536 ranges with scratch slots, so the stream and hybrid forms
-# also sum those rows whole, with the whole workgroup of the range each begins in
+# row tiles, the tuned stream ranges (1024 and 2048 nonzeros), hybrid tiles and
+# merge-path windows; at this size every long row from about p = 2^26 (ranges of
+# 1024) or 2^27 (2048) on has pieces past the 65536 ranges with scratch slots, so
+# the stream and hybrid forms also sum those rows whole, with the whole workgroup
+# of the range each begins in
 _SPMV_HUGE = [TUNED["c1"], TEST_SCHEDULES[0], TUNED["c3a"], TUNED["c3b"], NOALLOC_SCHEDULE,
               MERGE_TEST_SCHEDULES[1]]
 

@@ -31,15 +31,16 @@ TUNED: Dict[str, Config] = {
     "c2": Config(tile_size=128, threads_per_row=4, unroll=2, vector_width=1, block_size=256),
     # skewed rows, stream ranges: every workgroup takes an equal range of B x U
     # nonzeros and sums, from LDS, the rows that end in it.
-    # c3a (power-law rows, half of them one nonzero long): ranges of 4096 (1024
-    # lanes x 4), rows summed by 2-lane groups; 11.4 us against 11.7 with 4-lane
-    # groups, 11.6 with one lane per row and 12.1 for ranges of 2048, 13.6-14.1 for the
-    # best hybrid tiles (T64/TPR4/U4/B256) and 17.4 for row tiles alone (interleaved
-    # repeats on one box).
+    # c3a (power-law rows, half of them one nonzero long): ranges of 1024 (256 lanes
+    # x 4), one lane per short row; 776 workgroups, all resident at once (three per
+    # CU). Fastest of all 116 legal stream schedules: 11.25 us against 11.33 for 2-lane
+    # groups at B256 and 11.37 for ranges of 4096 at 2-lane groups (T512/TPR2/U4/B1024),
+    # 13.6-14.1 for the best hybrid tiles (T64/TPR4/U4/B256) and 17.4 for row tiles
+    # alone (interleaved repeats on one box).
     # c3b (1% of rows 2000 long, the rest 4): ranges of 2048 (512 lanes x 4), one
     # lane per short row; 6.9-7.1 us against 7.4-7.7 for the best hybrid tiles
     # (T128/TPR4/U2/B512) and 10.6 for the best row tiles (T32/TPR32/U2/B1024)
-    "c3a": Config(tile_size=512, threads_per_row=2, unroll=4, vector_width=1, block_size=1024,
+    "c3a": Config(tile_size=256, threads_per_row=1, unroll=4, vector_width=1, block_size=256,
                   balance="stream"),
     "c3b": Config(tile_size=512, threads_per_row=1, unroll=4, vector_width=1, block_size=512,
                   balance="stream"),
