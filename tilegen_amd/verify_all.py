@@ -30,6 +30,7 @@ from typing import Any, Dict, List, Optional, Sequence
 from .codegen import Config
 from .env import probe
 from .matrices import build_corpus, corpus_classes
+from .schedules import TUNED
 from .verify import verify
 
 __all__ = ["KERNELS", "CONFIGS", "BALANCE_CONFIGS", "SORTED_CONFIGS", "BUG_CONFIG", "run",
@@ -52,12 +53,12 @@ BALANCE_CONFIGS = [
     Config(tile_size=16, threads_per_row=8, unroll=2, vector_width=1, block_size=128,
            balance=b) for b in ("nnz", "hybrid", "stream")
 ]
-# HIP only: row tiles whose first-step gathers are sorted by column in LDS
+# HIP only: row tiles whose first-step gathers are sorted by column in LDS (a small
+# tile and the tuned c1 schedule)
 SORTED_CONFIGS = [
     Config(tile_size=64, threads_per_row=4, unroll=4, vector_width=1, block_size=256,
            gather="sorted"),
-    Config(tile_size=224, threads_per_row=4, unroll=4, vector_width=1, block_size=512,
-           gather="sorted"),
+    TUNED["c1"],
 ]
 
 
