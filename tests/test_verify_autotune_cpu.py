@@ -157,6 +157,32 @@ def test_write_outputs_schema(tmp_path):
     assert 0 < len(data["top5"]["tiny"]) <= 5
     raw = json.load(open(str(full / "autotune.json")))
     assert raw["results"][0]["records"]
+    assert data["results"][0]["mode"] == "random" and data["results"][0]["candidates"] == 2
+
+
+def test_write_outputs_tells_sorted_from_direct(tmp_path):
+    """A sorted-gather schedule and its direct twin share T/TPR/U/V/B: the CSV rows
+    carry the gather form (and the balance form) so they stay apart."""
+    metrics = {"ms_mean": 1.0, "ms_min": 1.0, "ms_median": 1.0, "gflops": 1.0,
+               "bandwidth_gbs": 1.0, "compulsory_gbs": 1.0, "max_abs_err": 0.0,
+               "tolerance": 1.0, "ok": True, "speedup_vs_naive": 1.0}
+    direct = Config(tile_size=64, threads_per_row=4, unroll=4, block_size=256)
+    twins = [direct, Config(**{**direct.to_dict(), "gather": "sorted"}),
+             Config(**{**direct.to_dict(), "balance": "stream"})]
+    recs = [dict(metrics, kernel="spmv", matrix_class="m", config=c.to_dict()) for c in twins]
+    res = {"kernel": "spmv", "matrix_class": "m", "backend": "hip", "mode": "exhaustive",
+           "candidates": 3, "baseline": direct.to_dict(), "baseline_ms_min": 1.0,
+           "winner": twins[1].to_dict(), "winner_metrics": recs[1], "records": recs}
+    full = tmp_path / "full"
+    write_outputs([res], str(tmp_path), {"backend": "hip"}, [], full_outdir=str(full))
+    lines = open(str(full / "autotune.csv")).read().splitlines()
+    head = lines[0].split(",")
+    forms = [(r.split(",")[head.index("balance")], r.split(",")[head.index("gather")])
+             for r in lines[1:]]
+    assert forms == [("rows", "direct"), ("rows", "sorted"), ("stream", "direct")]
+    from tilegen_amd.tune_all import render_markdown
+    md = render_markdown([res], "hip")
+    assert "| m | spmv | exhaustive | T64/TPR4/U4/V1/B256/sorted |" in md
 
 
 def test_bench_openmp_leg_on_cpu():
@@ -190,7 +216,7 @@ def test_sorted_space_matches_the_emitter(kernel):
     for c in limited:
         with pytest.raises(ValueError, match="sorted"):
             generate(k, c, "hip", write=False)
-    # the tuned c1 tile (224 rows) lies between the space's power-of-two tile sizes;
+    # the tuned c1 tile (240 rows) lies between the space's power-of-two tile sizes;
     # the same limits accept it
     from tilegen_amd.autotune import _sorted_reason
     assert TUNED["c1"].gather == "sorted" and _sorted_reason(TUNED["c1"]) is None

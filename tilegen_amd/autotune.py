@@ -39,7 +39,7 @@ import numpy as np
 import scipy.sparse as sp
 
 from . import codegen as _codegen
-from .codegen import Config
+from .codegen import LDS_LIMIT, Config
 from .dsl import standard_kernels
 from .verify import _SIGNATURES, _inputs_for, _load_matrix, _reference, compile_generated
 
@@ -62,7 +62,6 @@ SEARCH_SPACE: Dict[str, List[int]] = {
 BASELINE = Config(tile_size=32, threads_per_row=1, unroll=1, vector_width=1, block_size=128)
 
 _WAVE = 64
-_LDS_LIMIT = 160 * 1024  # LDS per CU on gfx950, all of which one workgroup may take
 # kernels whose schedules also come with merge-path windows, hybrid tiles and
 # stream ranges (Config.balance)
 MERGE_KERNELS = ("spmv", "fused_spmv_axpy")
@@ -98,7 +97,7 @@ def illegal_reason(cfg: Config) -> Optional[str]:
         return "tile_size (%d) < lane groups per block (%d): idle lanes" % (T, slots)
     if T > 8 * slots:
         return "tile_size (%d) > 8 rows per lane group (%d groups)" % (T, slots)
-    if 16 * (T + 1) > _LDS_LIMIT:
+    if 16 * (T + 1) > LDS_LIMIT:
         return "row pointers and row lists (%d B) exceed 160 KiB of LDS" % (16 * (T + 1))
     return None
 
@@ -194,8 +193,11 @@ def _stream_reason(cfg: Config) -> Optional[str]:
 
 def _sorted_reason(cfg: Config) -> Optional[str]:
     """A sorted tile holds its first step in registers (rows per lane group x
-    unroll <= 8) and its items in LDS (at most SORT_MAX_ITEMS)."""
-    from .codegen import SORT_MAX_ITEMS
+    unroll <= 8), its items in LDS (at most SORT_MAX_ITEMS), and those with the
+    tile's row pointers and lists within one workgroup's LDS."""
+    from .codegen import SORT_MAX_ITEMS, _lowering, _plan, launch_geometry
+    from .dsl import standard_kernels
+    from .passes import run_pipeline
     slots = cfg.block_size // cfg.threads_per_row
     rows = -(-cfg.tile_size // slots)
     if rows * cfg.unroll > 8:
@@ -203,6 +205,11 @@ def _sorted_reason(cfg: Config) -> Optional[str]:
     if rows * cfg.unroll * cfg.block_size > SORT_MAX_ITEMS:
         return "sorted first step of %d items exceeds %d" % (
             rows * cfg.unroll * cfg.block_size, SORT_MAX_ITEMS)
+    k = run_pipeline(standard_kernels()["spmv"], dataclasses.replace(cfg, gather="sorted"),
+                     backend="hip")
+    lds = launch_geometry(_plan(k), _lowering(k)).lds_bytes
+    if lds > LDS_LIMIT:
+        return "sorted tile's LDS arrays (%d B) exceed 160 KiB" % lds
     return None
 
 
@@ -468,6 +475,7 @@ def tune(kernel_name: str, matrix, budget: int = 40, mode: str = "random",
     measured = [r for r in records if r.get("ms_min") and r.get("ok")]
     winner = min(measured, key=lambda r: r["ms_median"]) if measured else None
     return {"kernel": kernel_name, "matrix_class": cls, "backend": backend,
+            "mode": mode, "candidates": len(candidates),
             "baseline": candidates[0].to_dict(), "baseline_ms_min": base,
             "winner": winner["config"] if winner else None,
             "winner_metrics": winner, "records": records}
@@ -480,8 +488,8 @@ def ms_median_or(v: float) -> float:
 _METRIC_FIELDS = ["ms_mean", "ms_min", "ms_median", "gflops", "bandwidth_gbs",
                   "compulsory_gbs", "max_abs_err", "tolerance", "ok", "speedup_vs_naive"]
 _CSV_COLS = ["matrix_class", "kernel", "tile_size", "threads_per_row", "unroll",
-             "vector_width", "block_size", "balance", "ms_mean", "ms_min", "ms_median", "gflops",
-             "bandwidth_gbs", "compulsory_gbs", "max_abs_err", "ok", "speedup_vs_naive"]
+             "vector_width", "block_size", "balance", "gather", "ms_mean", "ms_min", "ms_median",
+             "gflops", "bandwidth_gbs", "compulsory_gbs", "max_abs_err", "ok", "speedup_vs_naive"]
 
 
 def _compact(record: Optional[Dict[str, Any]]) -> Optional[Dict[str, Any]]:
@@ -491,8 +499,9 @@ def _compact(record: Optional[Dict[str, Any]]) -> Optional[Dict[str, Any]]:
 
 
 def _flat(record: Dict[str, Any]) -> Dict[str, Any]:
+    # Config.to_dict leaves the default balance and gather out
     row = {"matrix_class": record["matrix_class"], "kernel": record["kernel"],
-           "balance": "rows"}   # Config.to_dict leaves the default balance out
+           "balance": "rows", "gather": "direct"}
     row.update(record["config"])
     row.update({k: record.get(k) for k in _METRIC_FIELDS if k in record})
     return row
@@ -518,6 +527,7 @@ def write_outputs(all_results: List[Dict[str, Any]], outdir: str, env: Dict[str,
     for res in all_results:
         cls = res["matrix_class"]
         compact.append({"kernel": res["kernel"], "matrix_class": cls,
+                        "mode": res.get("mode"), "candidates": res.get("candidates"),
                         "baseline": res["baseline"], "baseline_ms_min": res["baseline_ms_min"],
                         "winner": res["winner"], "winner_metrics": _compact(res["winner_metrics"])})
         best.setdefault(cls, {})[res["kernel"]] = {

@@ -73,11 +73,12 @@ from .ir import (
 __all__ = [
     "Config", "GeneratedKernel", "Lowering", "Plan", "LaunchGeometry", "generate",
     "emit_hip", "emit_hip_host", "emit_cpu", "launch_geometry", "abi_of",
-    "HIP_ARCH", "WAVE",
+    "HIP_ARCH", "WAVE", "LDS_LIMIT",
 ]
 
 HIP_ARCH = os.environ.get("TILEGEN_HIP_ARCH", "gfx950")
 WAVE = 64
+LDS_LIMIT = 160 * 1024  # LDS per CU on gfx950, all of which one workgroup may take
 
 _CTYPE = {"f64": "double", "f32": "float", "double": "double", "float": "float"}
 
@@ -726,29 +727,58 @@ def _hip_decls(args: List[Tuple[str, str]]) -> str:
     return ", ".join(out)
 
 
+def _lds_total(arrays: Sequence[Tuple[int, int]]) -> int:
+    """Bytes of LDS a kernel's ``__shared__`` arrays take, given as (element
+    bytes, elements): their sum rounded up to 16 bytes.  The compiler packs a
+    kernel's LDS variables by alignment and rounds the block up to the largest
+    alignment (8, or 16 where it widens an array for 128-bit accesses), so this
+    is the group segment size it reports, or at most 8 bytes more."""
+    total = sum(size * count for size, count in arrays)
+    return (total + 15) // 16 * 16
+
+
 def launch_geometry(plan: Plan, low: Lowering) -> LaunchGeometry:
-    """Rows per workgroup and LDS bytes of the HIP variant for this schedule."""
+    """Rows per workgroup and LDS bytes of the HIP variant for this schedule.
+
+    The LDS figure adds up every ``__shared__`` array the emitters declare for
+    the form (``_lds_total``); the kernels hold all of it statically."""
     B = min(low.block_size, 1024)
     tpr = max(1, low.threads_per_row)
     if plan.kind == "elementwise":
         return LaunchGeometry(B, B, 0, plan.row_extent)
     slots = max(1, B // tpr)
-    if plan.kind == "sparse_out":
-        return LaunchGeometry(low.tile if low.tiled else slots, B, 0, plan.row_extent)
+    waves = max(1, B // WAVE)
     rows = low.tile if low.tiled else slots
-    if plan.kind == "scalar_reduce" and low.tiled and low.balance == "stream":
+    if plan.kind == "sparse_out":
+        # the chunked and the wave-per-row paths each list their tile's long rows
+        lists = [(4, rows), (4, 1), (8, 1)] if low.tiled else []
+        return LaunchGeometry(rows, B, _lds_total(lists + lists), plan.row_extent)
+    if plan.kind == "row_dense_out":
+        V = 2 if low.vector_width >= 2 else 1
+        arrays = [(4, rows), (4, 1), (8, B * V), (8, 1)] if low.tiled else []
+        return LaunchGeometry(rows, B, _lds_total(arrays), plan.row_extent)
+    if plan.kind != "scalar_reduce" or not low.tiled:
+        return LaunchGeometry(rows, B, 0, plan.row_extent)
+    if low.balance == "stream":
         CH, RB = stream_chunk(low), stream_batch(low)
-        lds = 8 * CH + 8 * (RB + 1) + 4 * RB + 8 * 6 + 4 + 8 * max(1, B // WAVE)
+        lds = _lds_total([(8, CH), (8, RB + 1), (8, 8), (4, RB), (4, 1), (8, waves)])
         return LaunchGeometry(1, B, lds, plan.row_extent, CH, stream=True)
-    lds = 8 * (rows + 1) if (plan.kind == "scalar_reduce" and low.tiled) else 0
-    if plan.kind == "scalar_reduce" and low.tiled and low.gather == "sorted":
-        # the sort's bucket counts, sorted entries and operands (sort_buckets)
-        items = ((rows + slots - 1) // slots) * max(1, low.unroll) * B
+    # a merge-path batch is at least one row per lane group
+    tr = max(rows, slots) if low.balance == "nnz" else rows
+    arrays = [(8, tr + 1), (4, tr), (4, 1), (8, waves)]   # pointers, long rows, sums
+    if tpr <= 16:
+        arrays += [(4, tr), (4, 1)]                          # rows left to one wave each
+    if low.balance == "hybrid":
+        arrays += [(8, 9), (8, 3 * waves), (8, waves), (8, 2)]
+    if low.balance == "nnz":
+        arrays += [(8, 6)]                                   # the window's rows and bounds
+    if low.gather == "sorted":
+        # the sort's bucket counts, sorted entries, operands and wave totals
+        items = ((tr + slots - 1) // slots) * max(1, low.unroll) * B
         nb = sort_buckets(B)
-        lds += 4 * nb + 16 * items + 4 * (nb // 64)
-    chunk = hybrid_chunk(low) if (plan.kind == "scalar_reduce" and low.tiled
-                                  and low.balance == "hybrid") else 0
-    return LaunchGeometry(rows, B, lds, plan.row_extent, chunk)
+        arrays += [(4, nb), (8, items), (8, items), (4, nb // 64)]
+    chunk = hybrid_chunk(low) if low.balance == "hybrid" else 0
+    return LaunchGeometry(rows, B, _lds_total(arrays), plan.row_extent, chunk)
 
 
 def module_scratch(plan: Plan, low: Lowering) -> bool:
@@ -812,6 +842,11 @@ def _check_hip_schedule(plan: Plan, low: Lowering) -> None:
     if low.balance == "stream" and stream_chunk(low) > STREAM_MAX_CHUNK:
         raise ValueError("stream ranges hold at most %d nonzeros (block_size x unroll), got %d"
                          % (STREAM_MAX_CHUNK, stream_chunk(low)))
+    lds = launch_geometry(plan, low).lds_bytes
+    if lds > LDS_LIMIT:
+        form = "sorted row tile" if low.gather == "sorted" else "%s variant" % low.balance
+        raise ValueError("this %s (tile %d, block %d) declares %d B of LDS; a gfx950 "
+                         "workgroup holds at most %d" % (form, low.tile, B, lds, LDS_LIMIT))
 
 
 def _long_row_test(length: str, long_: int, huge: int) -> str:

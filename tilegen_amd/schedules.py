@@ -21,7 +21,7 @@ TUNED: Dict[str, Config] = {
     # instruction's 64 lanes share cache lines of x.  11.4 us against 11.6 for
     # 256 rows on 1024 lanes, 11.7 for 224 rows on 512 lanes (two rows per
     # group), 12.6 for the best direct-gather tiles (T16/TPR8/U2/B128)
-    # (interleaved repeats on one box; a sweep of all 310 legal sorted schedules
+    # (interleaved repeats on one box; a sweep of all 307 legal sorted schedules
     # found the 1024-lane form first).  Two workgroups of 960 lanes share a CU
     # (62 VGPRs, 67.5 KB of LDS each); two of 832 or 896 lanes did not, and took
     # 15.6-15.8 us
