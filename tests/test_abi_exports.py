@@ -196,7 +196,6 @@ def test_no_packed_fp32_in_generated_code(tmp_path):
     objdump = "/opt/rocm/llvm/bin/llvm-objdump"
     if not os.path.exists(objdump):
         pytest.skip("llvm-objdump not available")
-    from tilegen_amd.verify import cache_dir
     for kernel in ("spmv", "spmm", "sddmm"):
         gen = generate(standard_kernels()[kernel], Config(tile_size=64, threads_per_row=8,
                                                           unroll=2, vector_width=2,

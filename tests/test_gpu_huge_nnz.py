@@ -21,7 +21,6 @@ import numpy as np
 import pytest
 
 from tilegen_amd import runtime as rt
-from tilegen_amd.codegen import Config
 from tilegen_amd.schedules import MERGE_TEST_SCHEDULES, NOALLOC_SCHEDULE, TEST_SCHEDULES, TUNED
 from tilegen_amd.variant import Variant
 from tilegen_amd.verify import hiprtc_options

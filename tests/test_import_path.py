@@ -7,7 +7,6 @@ from __future__ import annotations
 
 import importlib
 
-import numpy as np
 import pytest
 
 # (module, names) as the reference's callers import them

@@ -444,7 +444,7 @@ def test_scratch_argument_form_of_scratch_modules(balance):
 
 def test_noalloc_kernel_source_geometry():
     from tilegen_amd.build import noalloc_kernel_source
-    from tilegen_amd.codegen import MERGE_CAP, hybrid_chunk
+    from tilegen_amd.codegen import MERGE_CAP
     from tilegen_amd.schedules import NOALLOC_SCHEDULE
     src = noalloc_kernel_source()
     cfg = NOALLOC_SCHEDULE

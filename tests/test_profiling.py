@@ -9,7 +9,6 @@ import csv
 import json
 import os
 
-import numpy as np
 import pytest
 
 from tilegen_amd import profiling as pf
@@ -74,7 +73,7 @@ def test_case_plan_counts_and_shared_grid(plans):
     # headline: check + warmup + host-timed steps + warmup + event-timed steps
     assert by["c1"][2] == 1 + 2 * pf.WARMUP + 2 * pf.STEPS and by["c1"][3] == pf.STEPS
     # the others: check + one launch per input copy + warmup + event-timed launches
-    from tilegen_amd.matrices import baseline_case, compulsory_bytes, make_baseline
+    from tilegen_amd.matrices import compulsory_bytes, make_baseline
     A = make_baseline("c2")
     copies = pf.bench_copies(compulsory_bytes("spmv", A.shape[0], A.shape[1], int(A.nnz), 1))
     assert copies == 25  # 27.2 MB a launch: 640 MiB of rotation

@@ -30,9 +30,7 @@ import itertools
 import json
 import os
 import random
-import statistics
 import time
-from dataclasses import asdict
 from typing import Any, Dict, List, Optional, Tuple
 
 import numpy as np

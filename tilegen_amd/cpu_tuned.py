@@ -18,7 +18,7 @@ import argparse
 import json
 import os
 import sys
-from typing import Dict, List, Sequence
+from typing import List, Sequence
 
 from .autotune import tune
 from .codegen import Config
