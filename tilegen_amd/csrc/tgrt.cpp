@@ -507,13 +507,15 @@ int tg_graph_end(void* stream, void** exec) {
   hipGraph_t graph = nullptr;
   // the capture is ended even when the caller gave no output, so the stream is usable again
   TG_HIP(hipStreamEndCapture(static_cast<hipStream_t>(stream), &graph), "hipStreamEndCapture");
+  // the captured graph is released whatever happens next (its executable, when one is
+  // made, does not need it); a failure to release it changes nothing for the caller
   if (!exec) {
-    if (graph) hipGraphDestroy(graph);
+    if (graph) (void)hipGraphDestroy(graph);
     return fail(-1, "tg_graph_end: null output");
   }
   hipGraphExec_t e = nullptr;
   const hipError_t err = hipGraphInstantiate(&e, graph, nullptr, nullptr, 0);
-  hipGraphDestroy(graph);
+  (void)hipGraphDestroy(graph);
   if (err != hipSuccess) return hip_fail(err, "hipGraphInstantiate");
   *exec = e;
   return 0;
