@@ -143,7 +143,8 @@ STREAM_TEST_SCHEDULES: List[Config] = [
 
 # Row tiles whose first-step gathers are sorted in LDS (gather "sorted"): one to
 # eight rows per lane group, odd and even unroll, lane groups of 1 to 64 lanes,
-# blocks of 1, 3, 8 and 16 waves (64 to 1024 buckets), 384 to 8192 sorted items.
+# blocks of 1, 3, 8 and 16 waves (64 to 1024 buckets), 384 to 8192 sorted items, and
+# the largest LDS footprint the space allows (151,760 B: 8192 items, 1025 pointers).
 SORTED_TEST_SCHEDULES: List[Config] = [
     Config(tile_size=256, threads_per_row=8, unroll=2, block_size=512, gather="sorted"),
     Config(tile_size=64, threads_per_row=4, unroll=2, block_size=256, gather="sorted"),
@@ -152,6 +153,7 @@ SORTED_TEST_SCHEDULES: List[Config] = [
     Config(tile_size=8, threads_per_row=64, unroll=8, block_size=512, gather="sorted"),
     Config(tile_size=24, threads_per_row=8, unroll=2, block_size=192, gather="sorted"),
     Config(tile_size=512, threads_per_row=8, unroll=2, block_size=1024, gather="sorted"),
+    Config(tile_size=1024, threads_per_row=2, unroll=4, block_size=1024, gather="sorted"),
 ]
 
 
