@@ -33,7 +33,7 @@ TUNED: Dict[str, Config] = {
     # nonzeros and sums, from LDS, the rows that end in it.
     # c3a (power-law rows, half of them one nonzero long): ranges of 1024 (256 lanes
     # x 4), one lane per short row; 776 workgroups, all resident at once (three per
-    # CU). Fastest of all 116 legal stream schedules: 11.25 us against 11.33 for 2-lane
+    # CU, four on eight of them: 20.6 KB of LDS each). Fastest of all 116 legal stream schedules: 11.25 us against 11.33 for 2-lane
     # groups at B256 and 11.37 for ranges of 4096 at 2-lane groups (T512/TPR2/U4/B1024),
     # 13.6-14.1 for the best hybrid tiles (T64/TPR4/U4/B256) and 17.4 for row tiles
     # alone (interleaved repeats on one box).
