@@ -27,8 +27,12 @@ TUNED: Dict[str, Config] = {
     # 15.6-15.8 us
     "c1": Config(tile_size=240, threads_per_row=4, unroll=4, vector_width=1, block_size=960,
                  gather="sorted"),
-    # 7 nonzeros per row: 4 lanes x 2
-    "c2": Config(tile_size=128, threads_per_row=4, unroll=2, vector_width=1, block_size=256),
+    # 7 nonzeros per row: 4 lanes x 2, two rows per lane group; tiles of 160 rows on
+    # 320 lanes make 1250 workgroups, so the fullest CU holds 5 against a mean of 4.9
+    # (tiles of 128 rows: 1563, 7 against 6.1). 6.44 us against 6.64-6.73 for
+    # T128/TPR4/U2/B256, the fastest of the power-of-two space, 6.66 for T288/B576 and
+    # 6.91-8.10 for other lane groups at 320 lanes (interleaved repeats on one box)
+    "c2": Config(tile_size=160, threads_per_row=4, unroll=2, vector_width=1, block_size=320),
     # skewed rows, stream ranges: every workgroup takes an equal range of B x U
     # nonzeros and sums, from LDS, the rows that end in it.
     # c3a (power-law rows, half of them one nonzero long): ranges of 1024 (256 lanes
