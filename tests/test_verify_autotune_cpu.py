@@ -221,3 +221,18 @@ def test_sorted_space_matches_the_emitter(kernel):
     from tilegen_amd.autotune import _sorted_reason
     assert TUNED["c1"].gather == "sorted" and _sorted_reason(TUNED["c1"]) is None
     generate(k, TUNED["c1"], "hip", write=False)
+
+
+def test_tune_includes_tuned_schedules_outside_the_space():
+    """c1's and c2's tuned schedules lie between the space's powers of two; they are
+    legal, and ``include`` puts them among the candidates right after the baseline."""
+    import random
+    from tilegen_amd.autotune import _candidate_configs
+    from tilegen_amd.schedules import TUNED
+    extra = [TUNED["c1"], TUNED["c2"]]
+    legal = {c.hash() for c, r in enumerate_configs("spmv") if r is None}
+    assert all(c.hash() not in legal for c in extra)   # not in the space itself
+    assert all(illegal_reason_for("spmv", c) is None for c in extra)
+    cands = _candidate_configs("spmv", 8, 6, "random", random.Random(0), extra, "hip")
+    assert [c.hash() for c in cands[1:3]] == [c.hash() for c in extra]
+    assert cands[0].hash() == BASELINE.hash()
